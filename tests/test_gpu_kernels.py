@@ -1,0 +1,236 @@
+"""GPU parity of each kernel against the CPU oracle, through the C ABI (marked gpu).
+
+Bars: bit-exact for the Q8_1 bytes, the integer sub-block sums, the routing ids, the grouping and sort tables and the
+prefill activation planes; float outputs of a dot product within 1e-5 relative (the same integer sums, a different
+float summation order); a whole layer within 1e-3 relative L2 of the oracle fed the same int8 activation codes.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from tinystrata_amd import ops
+from tinystrata_amd._lib import IQ3_S, IQ3_XXS, Q4_K, Q8_0
+
+from gpu_util import dev, experts, host, rel_l2
+
+pytestmark = pytest.mark.gpu
+TYPES = (IQ3_XXS, IQ3_S, Q4_K, Q8_0)
+
+
+def test_quantize_q8_1_bytes_exact():
+    rng = np.random.default_rng(0)
+    x = rng.normal(0, 1, (9, 2048)).astype(np.float32)
+    x[1] = 0.0
+    x[2, ::97] *= 40.0                       # outliers
+    x[3, :32] = 1e9                          # d and s clamped to the largest half
+    x[4] = np.round(x[4] * 8) / 8            # many exact halves of d
+    got = host(ops.quantize_q8_1_rows(dev(x)))
+    assert (got == O.quantize_q8_1(x)).all()
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n", [256, 2048])
+def test_subblock_sums_exact(t, n):
+    rng = np.random.default_rng(t * 7 + n)
+    rows, ncols = 33, 3
+    w = ops.quantize_weights(t, rng.normal(0, 0.02, (rows, n)).astype(np.float32))
+    xq = O.quantize_q8_1(rng.normal(0, 1, (ncols, n)).astype(np.float32))
+    s, q = ops.subblock_sums(t, dev(w), n, rows, dev(xq), ncols)
+    es, eq = O.subblock_sums(t, w, n, rows, xq, ncols)
+    assert (host(s) == es).all() and (host(q) == eq).all()
+
+
+def test_subblock_sums_random_bytes_exact():
+    """Random block bytes exercise every grid index, sign pattern and sub-block scale (fixture weights)."""
+    from pathlib import Path
+
+    g = np.load(Path(__file__).resolve().parent / "golden" / "golden_rows.npz")
+    rng = np.random.default_rng(5)
+    for t in TYPES:
+        w = g[f"t{t}_n2048_nt4_w"]
+        rows = w.shape[0]
+        xq = O.quantize_q8_1(rng.normal(0, 1, (2, 2048)).astype(np.float32))
+        s, q = ops.subblock_sums(t, dev(w), 2048, rows, dev(xq), 2)
+        es, eq = O.subblock_sums(t, w, 2048, rows, xq, 2)
+        assert (host(s) == es).all(), t
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_in,n_out,ncols", [(2048, 96, 1), (2048, 40, 4), (512, 2048, 8), (768, 64, 3)])
+def test_mmvq(t, n_in, n_out, ncols):
+    if n_in % O.BLOCK[t][0]:
+        pytest.skip("not whole blocks")
+    rng = np.random.default_rng(n_in + n_out + t)
+    w = ops.quantize_weights(t, rng.normal(0, 0.02, (n_out, n_in)).astype(np.float32))
+    xq = O.quantize_q8_1(rng.normal(0, 1, (ncols, n_in)).astype(np.float32))
+    got = host(ops.iq_mmvq(t, dev(w), dev(xq), n_in, n_out, ncols))
+    exp = O.mmvq_q8_1(t, w, n_in, n_out, xq, ncols)
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * np.abs(exp).max())
+
+
+@pytest.mark.parametrize("E,k,T", [(256, 8, 1), (256, 8, 4), (128, 8, 512), (64, 4, 7), (512, 16, 3)])
+def test_router_topk(E, k, T):
+    rng = np.random.default_rng(E + k + T)
+    logits = rng.normal(0, 1, (T, E)).astype(np.float32)
+    ids, w = ops.native_router_topk(dev(logits), k)
+    eids, ew = O.router_topk(logits, k)
+    assert (host(ids) == eids).all()
+    np.testing.assert_allclose(host(w), ew, rtol=2e-6, atol=1e-7)
+
+
+def test_router_ties_and_nan():
+    logits = np.zeros((2, 64), np.float32)
+    logits[0, [5, 9, 40]] = 3.0
+    logits[1, :] = -50.0
+    logits[1, 7] = np.nan
+    ids, w = ops.native_router_topk(dev(logits), 4)
+    eids, ew = O.router_topk(logits, 4)
+    assert (host(ids) == eids).all()
+
+
+@pytest.mark.parametrize("n_tok,k,E", [(1, 8, 256), (4, 8, 256), (8, 8, 128), (64, 8, 256)])
+def test_group_tables_exact(n_tok, k, E):
+    rng = np.random.default_rng(n_tok * 13 + E)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    base, stride = 1 << 20, 4096
+    gp, gs, ng, ed, et = ops.group_entries(dev(ids), k, E, base, stride)
+    egp, egs, eg, eed, eet = O.group(ids, k, E, base, stride)
+    g = int(host(ng)[0])
+    assert g == eg
+    assert (host(gp)[:g].astype(np.uint64) == egp).all() and (host(gs)[:g + 1] == egs).all()
+    assert (host(ed) == eed).all() and (host(et) == eet).all()
+
+
+@pytest.mark.parametrize("n_tok,k,E", [(512, 8, 128), (4096, 8, 256), (3, 2, 64)])
+def test_route_sort_exact(n_tok, k, E):
+    rng = np.random.default_rng(n_tok + E)
+    bias = np.log(1.0 / (1 + rng.permutation(E)) ** 1.2)          # Zipf-skewed loads
+    logits = rng.normal(0, 1, (n_tok, E)) + bias
+    ids = np.argsort(-logits, axis=1)[:, :k].astype(np.int32)
+    b, ed, et, ri, mr = ops.route_sort(dev(ids), k, E)
+    eb, eed, eet, eri, emr = O.route_sort(ids, k, E)
+    assert (host(b) == eb).all() and (host(ed) == eed).all() and (host(et) == eet).all()
+    assert (host(ri) == eri).all() and int(host(mr)[0]) == emr
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_combine(shared):
+    rng = np.random.default_rng(3)
+    T, k, n = 4, 8, 2048
+    parts = rng.normal(0, 1, (T * k, n)).astype(np.float32)
+    wts = rng.random((T, k)).astype(np.float32)
+    x = rng.normal(0, 1, (T, n)).astype(np.float32)
+    prow = rng.permutation(T * k).astype(np.int32)
+    sh = rng.normal(0, 1, (T, n)).astype(np.float32) if shared else None
+    sg = rng.normal(0, 1, T).astype(np.float32) if shared else None
+    xd = dev(x)
+    ops.moe_combine(xd, dev(parts), dev(wts), k, prow=dev(prow), shared=None if sh is None else dev(sh),
+                    sgate=None if sg is None else dev(sg))
+    exp = O.combine(x, parts, wts, k, prow=prow, shared=sh, sgate=sg)
+    got = host(xd)
+    if shared:   # expf of the gate on the two sides may differ in the last bit
+        np.testing.assert_allclose(got, exp, rtol=1e-6, atol=1e-6)
+    else:        # the same products and FMAs in the same order
+        assert (got == exp).all()
+
+
+def test_mmq_quantize_planes_exact():
+    rng = np.random.default_rng(8)
+    rows, cols = 70, 512
+    x = rng.normal(0, 1, (100, cols)).astype(np.float32)
+    ids = rng.integers(0, 100, rows).astype(np.int32)
+    xq = host(ops.mmq_quantize(dev(x), dev(ids), Q4_K, cols, cols, rows))
+    rp = (rows + 63) // 64 * 64 + 64
+    r256 = lambda v: (v + 255) // 256 * 256
+    q = xq[: rp * cols].view(np.int8).reshape(rp, cols)
+    d = xq[r256(rp * cols): r256(rp * cols) + rp * cols // 32 * 4].view(np.float32).reshape(rp, cols // 32)
+    m0 = r256(rp * cols) + r256(rp * cols // 32 * 4)
+    m = xq[m0: m0 + rp * cols // 32 * 4].view(np.int32).reshape(rp, cols // 32)
+    ed, _, ecodes = O.q8_1_split(O.quantize_q8_1(x[ids]))
+    assert (q[:rows].reshape(-1, 32) == ecodes).all()
+    assert (d[:rows].ravel() == ed).all()
+    assert (m[:rows].ravel() == ecodes.astype(np.int32).sum(1)).all()
+    assert (q[rows:] == 0).all() and (d[rows:] == 0).all()
+
+
+# ------------------------------------------------------------------ grouped experts
+CASES = {
+    "iq3_2048x512": (IQ3_XXS, IQ3_S, 2048, 512),
+    "q8_0_2048x768": (Q8_0, Q8_0, 2048, 768),
+    "q4_k_2048x768": (Q4_K, Q4_K, 2048, 768),
+    "iq3_small": (IQ3_XXS, IQ3_S, 256, 256),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+@pytest.mark.parametrize("n_tok", [1, 4])
+def test_expert_grouped(case, n_tok):
+    gu, d, N, FF = CASES[case]
+    E, k = 32, 8
+    L, blobs, _ = experts(gu, d, N, FF, E)
+    Lo = O.layout(gu, d, N, FF)
+    stride = blobs.shape[1]
+    rng = np.random.default_rng(N + FF + n_tok)
+    x = rng.normal(0, 1, (n_tok, N)).astype(np.float32)
+    z = rng.normal(0, 1, E)
+    logits = (z[None, :] + 0.5 * rng.normal(0, 1, (n_tok, E))).astype(np.float32)   # overlapping experts
+    ids, _ = O.router_topk(logits, k)
+    blobs_d = dev(blobs.ravel())
+    n_ent = n_tok * k
+    gp, gs, ng, ed, et = ops.group_entries(dev(ids), k, E, blobs_d.data_ptr(), stride)
+    xq = ops.quantize_q8_1_rows(dev(x))
+    scratch = torch.zeros(ops.native_expert_scratch_bytes(n_ent, FF), dtype=torch.uint8, device="cuda")
+    out = torch.full((n_ent, N), float("nan"), device="cuda")
+    cap_groups = min(n_ent, E)
+    ops.native_expert_grouped(L, gp, gs, ng, ed, et, cap_groups, n_ent, xq, scratch, out)
+    got = host(out)
+    # the oracle on the same tables
+    _, egs, g, eed, eet = O.group(ids, k, E)
+    used = np.unique(ids)
+    hb = [blobs[x] for x in used]
+    xq_h = host(xq)
+    h, hq = O.expert_gu(Lo, hb, egs, eet, xq_h)
+    sc = host(scratch)
+    fa = (n_ent * FF * 4 + 255) // 256 * 256
+    gate = sc[:n_ent * FF * 4].view(np.float32).reshape(n_ent, FF)
+    up = sc[fa: fa + n_ent * FF * 4].view(np.float32).reshape(n_ent, FF)
+    # gate/up rows: the same integer sums, float order only
+    for e in range(n_ent):
+        tok = eet[e]
+        x_blob = blobs[ids.ravel()[eed[e]]]
+        eg = O.mmvq_q8_1(gu, x_blob, N, FF, xq_h[tok], 1)[0]
+        eu = O.mmvq_q8_1(gu, x_blob[Lo.up_off:], N, FF, xq_h[tok], 1)[0]
+        np.testing.assert_allclose(gate[e], eg, rtol=1e-5, atol=1e-5 * np.abs(eg).max())
+        np.testing.assert_allclose(up[e], eu, rtol=1e-5, atol=1e-5 * np.abs(eu).max())
+    hq_gpu = sc[ops.scratch_hq_offset(n_ent, FF): ops.scratch_hq_offset(n_ent, FF) + n_ent * FF // 32 * 36]
+    hq_gpu = hq_gpu.reshape(n_ent, -1)
+    # Q8_1 of the GPU's own SwiGLU output equals the oracle's but for values on a rounding edge
+    d_g, _, c_g = O.q8_1_split(hq_gpu)
+    d_o, _, c_o = O.q8_1_split(hq)
+    assert np.mean(c_g != c_o) < 1e-3 and np.mean(d_g != d_o) < 1e-2
+    # the down rows fed the GPU's int8 codes: float order only
+    down_same = O.expert_down(Lo, hb, egs, eed, hq_gpu, n_ent)
+    np.testing.assert_allclose(got, down_same, rtol=1e-5, atol=1e-5 * np.abs(down_same).max())
+    # end to end against the oracle's own codes
+    down_own = O.expert_down(Lo, hb, egs, eed, hq, n_ent)
+    assert rel_l2(got, down_own) < 1e-3
+
+
+def test_expert_grouped_grid_groups_invariant():
+    gu, d, N, FF = CASES["iq3_small"]
+    E, k, n_tok = 16, 4, 4
+    L, blobs, _ = experts(gu, d, N, FF, E)
+    rng = np.random.default_rng(1)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(n_tok)]).astype(np.int32)
+    blobs_d = dev(blobs.ravel())
+    gp, gs, ng, ed, et = ops.group_entries(dev(ids), k, E, blobs_d.data_ptr(), blobs.shape[1])
+    xq = ops.quantize_q8_1_rows(dev(rng.normal(0, 1, (n_tok, N)).astype(np.float32)))
+    n_ent = n_tok * k
+    outs = []
+    for gg in (0, 1, 3):
+        scratch = torch.zeros(ops.native_expert_scratch_bytes(n_ent, FF), dtype=torch.uint8, device="cuda")
+        out = torch.zeros((n_ent, N), device="cuda")
+        ops.native_expert_grouped(L, gp, gs, ng, ed, et, min(n_ent, E), n_ent, xq, scratch, out, grid_groups=gg)
+        outs.append(host(out))
+    assert (outs[0] == outs[1]).all() and (outs[0] == outs[2]).all()

@@ -1,0 +1,115 @@
+"""ctypes binding of libtsx_moe.so (the C ABI declared in include/tsx_moe.h).
+
+The library is built in-tree by tinystrata_amd.build; nothing here falls back to another implementation: a missing
+library raises, so a GPU run can never pass on a silent host or PyTorch path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libtsx_moe.so"
+
+ABI_VERSION = 1
+TSX_OK, TSX_ERR_UNSUPPORTED, TSX_ERR_ARG = 0, -1, -2
+
+# type ids (ggml's)
+Q8_0, Q8_1, Q4_K, Q8_K, IQ3_XXS, IQ3_S = 8, 9, 12, 15, 18, 21
+
+
+class ExpertLayout(C.Structure):
+    """tsx_expert_layout: the [gate | up | down] blob of one expert (reference NativeExpertLayout)."""
+
+    _fields_ = [
+        ("gu_type", C.c_int32),
+        ("d_type", C.c_int32),
+        ("n_embd", C.c_int64),
+        ("n_ff", C.c_int64),
+        ("gu_row", C.c_uint64),
+        ("d_row", C.c_uint64),
+        ("up_off", C.c_uint64),
+        ("down_off", C.c_uint64),
+        ("bytes", C.c_uint64),
+    ]
+
+
+class MmqProduct(C.Structure):
+    """tsx_mmq_product: one grouped prompt product (reference prefill::mmq::Product)."""
+
+    _fields_ = [
+        ("w", C.c_void_p),
+        ("type", C.c_int32),
+        ("n", C.c_int32),
+        ("w_rows", C.c_int64),
+        ("w_cols", C.c_int64),
+        ("expert_bytes", C.c_uint64),
+        ("xq", C.c_void_p),
+        ("bounds", C.c_void_p),
+        ("ids", C.c_void_p),
+        ("total_rows", C.c_int64),
+        ("max_rows", C.c_int64),
+        ("dst", C.c_void_p),
+        ("ld_dst", C.c_int64),
+    ]
+
+
+P, I32, I64, U64, SZ = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_size_t
+
+# name -> (restype, argtypes); the list is the whole C ABI, checked against include/tsx_moe.h by the tests
+SIGNATURES = {
+    "tsx_moe_abi": (I32, []),
+    "tsx_moe_init": (I32, [I32]),
+    "tsx_moe_last_error": (C.c_char_p, []),
+    "tsx_moe_row_bytes": (SZ, [I32, I64]),
+    "tsx_moe_expert_layout": (I32, [I32, I32, I64, I64, C.POINTER(ExpertLayout)]),
+    "tsx_moe_expert_supported": (I32, [I32, I32, I64, I64]),
+    "tsx_moe_expert_scratch_bytes": (SZ, [I64, I64]),
+    "tsx_moe_expert_scratch_hq_offset": (SZ, [I64, I64]),
+    "tsx_moe_quantize_q8_1": (I32, [P, I64, I64, P, P]),
+    "tsx_moe_swiglu_quantize_q8_1": (I32, [P, P, I64, P, P]),
+    "tsx_moe_expert_grouped": (I32, [C.POINTER(ExpertLayout), P, P, P, P, P, I64, I64, P, P, P, P, I64]),
+    "tsx_moe_mmvq": (I32, [I32, P, P, P, I32, I32, I32, P]),
+    "tsx_moe_router_topk": (I32, [P, P, P, I32, I32, I32, P]),
+    "tsx_moe_group": (I32, [P, I32, I32, I32, P, U64, P, P, P, P, P, P]),
+    "tsx_moe_route_sort": (I32, [P, I32, I32, I32, P, P, P, P, P, P]),
+    "tsx_moe_combine": (I32, [P, P, P, P, I32, P, P, I32, I32, I32, P]),
+    "tsx_moe_mmq_q8_bytes": (SZ, [I64, I64]),
+    "tsx_moe_mmq_quantize": (I32, [P, P, P, I32, I64, I64, I64, P]),
+    "tsx_moe_mmq_run": (I32, [C.POINTER(MmqProduct), P]),
+    "tsx_moe_mmq_swiglu": (I32, [P, P, I64, I64, I32, P]),
+    "tsx_moe_subblock_sums": (I32, [I32, P, I64, I64, P, I64, P, P, P]),
+    "tsx_moe_quantize_weights": (I32, [I32, P, I64, I64, P]),
+}
+
+_lib: C.CDLL | None = None
+
+
+class TsxError(RuntimeError):
+    def __init__(self, what: str, rc: int, msg: str):
+        super().__init__(f"{what} failed ({rc}): {msg}")
+        self.rc = rc
+
+
+def lib() -> C.CDLL:
+    """The loaded library; raises FileNotFoundError when it has not been built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build it with `python -m tinystrata_amd.build` (hipcc, gfx950)"
+            )
+        h = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(h, name)
+            f.restype = res
+            f.argtypes = args
+        abi = h.tsx_moe_abi()
+        if abi // 100000 != ABI_VERSION or abi % 100000 != C.sizeof(MmqProduct):
+            raise RuntimeError(f"{LIB_PATH}: ABI {abi} does not match this binding")
+        _lib = h
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != TSX_OK:
+        raise TsxError(what, rc, lib().tsx_moe_last_error().decode(errors="replace"))

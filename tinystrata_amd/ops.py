@@ -1,0 +1,188 @@
+"""Python mirror of the reference's operator API for the MoE expert path, over libtsx_moe.so.
+
+Names and argument meanings follow TinyStrata's C++ headers (include/strata/kernels/iq_kernels.hpp,
+native_mmvq.hpp, native_router.hpp, include/strata/prefill/moe_mmq.hpp); buffers are torch tensors in device
+memory (PyTorch is only the allocator and the stream here), and every call enqueues on the current stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from ._lib import IQ3_S, IQ3_XXS, Q4_K, Q8_0, ExpertLayout, MmqProduct, check, lib
+
+WEIGHT_TYPES = (Q8_0, Q4_K, IQ3_XXS, IQ3_S)
+Q8_1_BLOCK_BYTES = 36
+
+
+def _p(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("device tensors only")
+    return t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+# ------------------------------------------------------------------ formats
+def iq_supported(ggml_type: int) -> bool:
+    return ggml_type in WEIGHT_TYPES
+
+
+def iq_row_bytes(ggml_type: int, n: int) -> int:
+    return lib().tsx_moe_row_bytes(ggml_type, n)
+
+
+def native_expert_supported(gu_type: int, d_type: int, n_embd: int, n_ff: int) -> bool:
+    return bool(lib().tsx_moe_expert_supported(gu_type, d_type, n_embd, n_ff))
+
+
+def native_expert_layout(gu_type: int, d_type: int, n_embd: int, n_ff: int) -> ExpertLayout:
+    L = ExpertLayout()
+    check(lib().tsx_moe_expert_layout(gu_type, d_type, n_embd, n_ff, C.byref(L)), "native_expert_layout")
+    return L
+
+
+def native_expert_scratch_bytes(cap_entries: int, n_ff: int) -> int:
+    return lib().tsx_moe_expert_scratch_bytes(cap_entries, n_ff)
+
+
+def scratch_hq_offset(cap_entries: int, n_ff: int) -> int:
+    return lib().tsx_moe_expert_scratch_hq_offset(cap_entries, n_ff)
+
+
+# ------------------------------------------------------------------ activations
+def quantize_q8_1_rows(x: torch.Tensor, out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """x [rows, cols] float32 -> Q8_1 blocks, uint8 [rows, cols/32*36]."""
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty((rows, cols // 32 * Q8_1_BLOCK_BYTES), dtype=torch.uint8, device=x.device)
+    check(lib().tsx_moe_quantize_q8_1(_p(x), rows, cols, _p(out), _stream(stream)), "quantize_q8_1_rows")
+    return out
+
+
+def native_swiglu_quantize_q8_1(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor | None = None, stream=None):
+    n = gate.numel()
+    if out is None:
+        out = torch.empty(n // 32 * Q8_1_BLOCK_BYTES, dtype=torch.uint8, device=gate.device)
+    check(lib().tsx_moe_swiglu_quantize_q8_1(_p(gate), _p(up), n, _p(out), _stream(stream)), "native_swiglu_quantize_q8_1")
+    return out
+
+
+# ------------------------------------------------------------------ decode
+def native_expert_grouped(L: ExpertLayout, grp_ptr, grp_start, n_groups, ent_dst, ent_tok, cap_groups: int,
+                          cap_entries: int, x_q8_1, scratch, out, grid_groups: int = 0, stream=None) -> None:
+    check(lib().tsx_moe_expert_grouped(C.byref(L), _p(grp_ptr), _p(grp_start), _p(n_groups), _p(ent_dst), _p(ent_tok),
+                                       cap_groups, cap_entries, _p(x_q8_1), _p(scratch), _p(out), _stream(stream),
+                                       grid_groups), "native_expert_grouped")
+
+
+def iq_mmvq(ggml_type: int, w, x_q8_1, n_in: int, n_out: int, ncols: int, y=None, stream=None) -> torch.Tensor:
+    """y[c][r] = W[r] . x[c] (ncols 1..8)."""
+    if y is None:
+        y = torch.empty((ncols, n_out), dtype=torch.float32, device=w.device)
+    check(lib().tsx_moe_mmvq(ggml_type, _p(w), _p(x_q8_1), _p(y), n_in, n_out, ncols, _stream(stream)), "iq_mmvq")
+    return y
+
+
+native_mmvq = iq_mmvq
+
+
+# ------------------------------------------------------------------ routing
+def native_router_topk(logits: torch.Tensor, k: int, ids=None, weights=None, stream=None):
+    n_tok, n_expert = logits.shape
+    if ids is None:
+        ids = torch.empty((n_tok, k), dtype=torch.int32, device=logits.device)
+    if weights is None:
+        weights = torch.empty((n_tok, k), dtype=torch.float32, device=logits.device)
+    check(lib().tsx_moe_router_topk(_p(logits), _p(ids), _p(weights), n_expert, k, n_tok, _stream(stream)),
+          "native_router_topk")
+    return ids, weights
+
+
+def group_entries(ids: torch.Tensor, k: int, n_expert: int, blobs_ptr: int, stride: int, bufs=None, stream=None):
+    """Decode grouping (k_group): returns grp_ptr, grp_start, n_groups, ent_dst, ent_tok (device tensors)."""
+    n_ent = ids.numel()
+    cap = min(n_ent, n_expert)
+    dev = ids.device
+    if bufs is None:
+        bufs = (torch.empty(cap, dtype=torch.int64, device=dev), torch.empty(cap + 1, dtype=torch.int32, device=dev),
+                torch.empty(1, dtype=torch.int32, device=dev), torch.empty(n_ent, dtype=torch.int32, device=dev),
+                torch.empty(n_ent, dtype=torch.int32, device=dev))
+    gp, gs, ng, ed, et = bufs
+    check(lib().tsx_moe_group(_p(ids), n_ent, k, n_expert, blobs_ptr, stride, _p(gp), _p(gs), _p(ng), _p(ed), _p(et),
+                              _stream(stream)), "group_entries")
+    return bufs
+
+
+def route_sort(ids: torch.Tensor, k: int, n_expert: int, bufs=None, stream=None):
+    """The prompt's expert sort: bounds [E+1], ent_dst, ent_tok, rinv [n_ent], max_rows [1]."""
+    n_ent = ids.numel()
+    dev = ids.device
+    if bufs is None:
+        bufs = (torch.empty(n_expert + 1, dtype=torch.int32, device=dev), torch.empty(n_ent, dtype=torch.int32, device=dev),
+                torch.empty(n_ent, dtype=torch.int32, device=dev), torch.empty(n_ent, dtype=torch.int32, device=dev),
+                torch.empty(1, dtype=torch.int32, device=dev))
+    b, ed, et, ri, mr = bufs
+    check(lib().tsx_moe_route_sort(_p(ids), n_ent, k, n_expert, _p(b), _p(ed), _p(et), _p(ri), _p(mr), _stream(stream)),
+          "route_sort")
+    return bufs
+
+
+def moe_combine(x, parts, wts, k: int, prow=None, shared=None, sgate=None, sg_stride: int = 1, stream=None) -> None:
+    """x[t] += sum_j w[t][j] parts[p(t,j)] (+ sigmoid(sgate[t]) shared[t]), in place."""
+    n_tok, n = x.shape
+    check(lib().tsx_moe_combine(_p(x), _p(parts), _p(prow), _p(wts), k, _p(shared), _p(sgate), sg_stride, n, n_tok,
+                                _stream(stream)), "moe_combine")
+
+
+# ------------------------------------------------------------------ prefill
+def mmq_q8_bytes(rows: int, cols: int) -> int:
+    return lib().tsx_moe_mmq_q8_bytes(rows, cols)
+
+
+def mmq_quantize(x, ids, ggml_type: int, cols: int, ld: int, rows: int, xq=None, stream=None) -> torch.Tensor:
+    if xq is None:
+        xq = torch.empty(mmq_q8_bytes(rows, cols), dtype=torch.uint8, device=x.device)
+    check(lib().tsx_moe_mmq_quantize(_p(x), _p(ids), _p(xq), ggml_type, cols, ld, rows, _stream(stream)), "mmq_quantize")
+    return xq
+
+
+def mmq_run(w, ggml_type: int, w_rows: int, w_cols: int, expert_bytes: int, n: int, xq, bounds, ids, total_rows: int,
+            dst, ld_dst: int, max_rows: int = 0, stream=None) -> None:
+    p = MmqProduct(w=_p(w), type=ggml_type, n=n, w_rows=w_rows, w_cols=w_cols, expert_bytes=expert_bytes, xq=_p(xq),
+                   bounds=_p(bounds), ids=_p(ids), total_rows=total_rows, max_rows=max_rows, dst=_p(dst), ld_dst=ld_dst)
+    check(lib().tsx_moe_mmq_run(C.byref(p), _stream(stream)), "mmq_run")
+
+
+def mmq_swiglu(gu, rows: int, n_ff: int, interleaved: bool = False, h=None, stream=None) -> torch.Tensor:
+    if h is None:
+        h = torch.empty((rows, n_ff), dtype=torch.float32, device=gu.device)
+    check(lib().tsx_moe_mmq_swiglu(_p(gu), _p(h), rows, n_ff, int(interleaved), _stream(stream)), "mmq_swiglu")
+    return h
+
+
+# ------------------------------------------------------------------ checks and data
+def subblock_sums(ggml_type: int, w, n_in: int, n_rows: int, x_q8_1, ncols: int, stream=None):
+    nsub = n_in // 32
+    sums = torch.empty((n_rows, ncols, nsub), dtype=torch.int32, device=w.device)
+    qsums = torch.empty((n_rows, ncols, nsub), dtype=torch.int32, device=w.device)
+    check(lib().tsx_moe_subblock_sums(ggml_type, _p(w), n_in, n_rows, _p(x_q8_1), ncols, _p(sums), _p(qsums),
+                                      _stream(stream)), "subblock_sums")
+    return sums, qsums
+
+
+def quantize_weights(ggml_type: int, x: np.ndarray) -> np.ndarray:
+    """Host: float32 [rows, cols] -> GGUF blocks uint8 [rows, row_bytes]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, cols = x.shape
+    rb = iq_row_bytes(ggml_type, cols)
+    out = np.empty((rows, rb), dtype=np.uint8)
+    check(lib().tsx_moe_quantize_weights(ggml_type, x.ctypes.data, rows, cols, out.ctypes.data), "quantize_weights")
+    return out
