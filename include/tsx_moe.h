@@ -95,6 +95,23 @@ TSX_API int tsx_moe_expert_grouped(const tsx_expert_layout* L, const uint64_t* g
 TSX_API int tsx_moe_mmvq(int type, const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                          void* stream);
 
+/* The whole decode MoE layer for 1..8 tokens in two launches: routing (tsx_moe_router_topk's arithmetic), grouping,
+ * Q8_1 of x, the grouped gate/up rows with SwiGLU + Q8_1, the down rows and the combine:
+ *   y[t] += sum_j wts[t][j] * expert(ids[t][j], x[t])  (first product, then FMA, pick order)
+ *         + sigmoid(sgate[t * sg_stride]) * expert(shared, x[t])          (when shared is not null)
+ * where expert(b, x) = down . Q8_1(silu(gate . Q8_1(x)) * (up . Q8_1(x))) of the blob at b; expert e's blob is at
+ * blobs + e * stride.  ids / wts [n_tok][k] receive the routing.  y may alias x.  Limits: n_embd <= 4096,
+ * n_ff <= 1024, n_tok * k <= 64, n_expert a multiple of 64 up to 512; blobs, stride and shared 16-byte aligned.
+ * scratch: tsx_moe_decode_layer_scratch_bytes(n_tok, k, n_ff) bytes, 256-byte aligned.
+ * Replaces the MoE block's call sequence at src/qwen35/q36_engine.cu:2821-2925: k_route_group
+ * (src/qwen35/q36_kernels.cuh:383-474), native_expert_grouped (src/kernels/cuda/iq_kernels.cu:2835-2982), the shared
+ * expert's mmvq / SwiGLU / mmvq (q36_engine.cu:2906-2913) and k_moe_out_small without the norm
+ * (q36_kernels.cuh:248-290). */
+TSX_API size_t tsx_moe_decode_layer_scratch_bytes(int n_tok, int k, int64_t n_ff);
+TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* L, const void* blobs, uint64_t stride, int n_expert, int k,
+                                 int n_tok, const float* logits, const float* x, const void* shared, const float* sgate,
+                                 int sg_stride, float* y, int32_t* ids, float* wts, void* scratch, void* stream);
+
 /* ------------------------------------------------------------------------------------------------ routing */
 /* logits [n_tok][n_expert] -> ids [n_tok][k] and weights [n_tok][k]: softmax, k rounds of argmax (ties to the
  * lower id; NaN probabilities never win), weights renormalized by max(sum of the picks, 6.1035e-5).

@@ -36,9 +36,9 @@ def make_layer(gu, d, N, FF, E, shared, distinct=8, seed=0):
     return L, p, order, W
 
 
-def run_layer(W, k, x, logits, sgate):
+def run_layer(W, k, x, logits, sgate, fused=True):
     T, N = x.shape
-    layer = moe.MoELayer(W, k, T, torch.device("cuda"))
+    layer = moe.MoELayer(W, k, T, torch.device("cuda"), fused=fused)
     y = torch.zeros((T, N), device="cuda")
     layer(dev(x), dev(logits), None if sgate is None else dev(sgate), y)
     return host(y), host(layer.ids)
@@ -61,12 +61,15 @@ def inputs(cfg, T, E, N, seed):
     return x, logits.astype(np.float32), sgate
 
 
+@pytest.mark.parametrize("fused", [True, False], ids=["two_launch", "kernel_by_kernel"])
 @pytest.mark.parametrize("cfg", list(CONFIGS))
-def test_layer_against_oracle(cfg):
+def test_layer_against_oracle(cfg, fused):
     gu, d, N, FF, E, k, shared, T = CONFIGS[cfg]
+    if not fused and T > 8:
+        pytest.skip("prompt chunks have one path")
     L, p, order, W = make_layer(gu, d, N, FF, E, shared)
     x, logits, sgate = inputs(cfg, T, E, N, seed=len(cfg))
-    got, ids = run_layer(W, k, x, logits, sgate if shared else None)
+    got, ids = run_layer(W, k, x, logits, sgate if shared else None, fused=fused)
     Lo = O.layout(gu, d, N, FF)
     blobs = p[order]
     sh = p[len(p) - 1] if shared else None
@@ -97,3 +100,68 @@ def test_full_prefill_sampled_tokens(cfg, T, E, k, shared, gu, d, FF):
     err = rel_l2(got[sample], y0)
     print(f"{cfg}: {T} tokens, sampled rows rel L2 {err:.2e}")
     assert err < 1e-3
+
+
+DECODE_CASES = [
+    # (gu, d, N, FF, E, k, shared, T): the edges of the two-launch decode layer
+    (IQ3_XXS, IQ3_S, 2048, 512, 256, 8, True, 8),     # 64 entries, the most one call takes
+    (Q4_K, Q4_K, 2048, 768, 128, 8, True, 2),         # 16-row chunks of gate/up rows
+    (Q8_0, Q8_0, 2048, 768, 64, 4, True, 3),          # 8-row chunks
+    (IQ3_S, IQ3_XXS, 4096, 256, 512, 2, False, 5),    # widest rows, 512 experts
+    (IQ3_XXS, Q8_0, 2048, 1024, 64, 1, True, 1),      # top-1, widest FF
+]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=lambda c: f"{c[0]}-{c[1]}-N{c[2]}-FF{c[3]}-E{c[4]}-k{c[5]}-T{c[7]}")
+def test_decode_layer_edges(case):
+    gu, d, N, FF, E, k, shared, T = case
+    L, p, order, W = make_layer(gu, d, N, FF, E, shared, distinct=5, seed=3)
+    x, logits, sgate = inputs("edge", T, E, N, seed=N + FF + E + T)
+    got, ids = run_layer(W, k, x, logits, sgate if shared else None)
+    Lo = O.layout(gu, d, N, FF)
+    sh = p[len(p) - 1] if shared else None
+    y0, eids, _ = O.moe_layer(0, Lo, x, logits, k, p[order], p.shape[1], sh, sgate if shared else None)
+    assert (ids == eids).all()
+    err = rel_l2(got, y0)
+    print(f"{case}: rel L2 {err:.2e}")
+    assert err < 1e-3
+
+
+def test_decode_layer_residual_alias_and_replay():
+    """y may alias x (x <- x + moe(x)); a captured graph replays to the same bits as the eager call, every time."""
+    gu, d, N, FF, E, k, shared, T = CONFIGS["c3_verify_iq3"]
+    L, p, order, W = make_layer(gu, d, N, FF, E, shared)
+    x, logits, sgate = inputs("c3", T, E, N, seed=11)
+    ref, _, _ = O.moe_layer(0, O.layout(gu, d, N, FF), x, logits, k, p[order], p.shape[1], p[len(p) - 1], sgate)
+    layer = moe.MoELayer(W, k, T, torch.device("cuda"))
+    xd, ld, sd = dev(x), dev(logits), dev(sgate)
+    buf = xd.clone()
+    layer(buf, ld, sd, buf)
+    eager = host(buf)
+    assert rel_l2(eager.astype(np.float64) - x, ref) < 1e-3
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        buf.copy_(xd)
+        layer(buf, ld, sd, buf)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        buf.copy_(xd)
+        layer(buf, ld, sd, buf)
+    for _ in range(3):
+        g.replay()
+        assert (host(buf) == eager).all()
+        buf.zero_()
+        torch.cuda.synchronize()
+
+
+def test_decode_layer_matches_kernel_by_kernel():
+    """The two launches and the reference's kernel-by-kernel sequence route identically and agree to float order."""
+    gu, d, N, FF, E, k, shared, T = CONFIGS["c3_verify_iq3"]
+    L, p, order, W = make_layer(gu, d, N, FF, E, shared)
+    x, logits, sgate = inputs("c3", T, E, N, seed=5)
+    a, ia = run_layer(W, k, x, logits, sgate, fused=True)
+    b, ib = run_layer(W, k, x, logits, sgate, fused=False)
+    assert (ia == ib).all()
+    assert rel_l2(a, b) < 1e-5

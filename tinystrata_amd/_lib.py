@@ -69,6 +69,8 @@ SIGNATURES = {
     "tsx_moe_swiglu_quantize_q8_1": (I32, [P, P, I64, P, P]),
     "tsx_moe_expert_grouped": (I32, [C.POINTER(ExpertLayout), P, P, P, P, P, I64, I64, P, P, P, P, I64]),
     "tsx_moe_mmvq": (I32, [I32, P, P, P, I32, I32, I32, P]),
+    "tsx_moe_decode_layer_scratch_bytes": (SZ, [I32, I32, I64]),
+    "tsx_moe_decode_layer": (I32, [C.POINTER(ExpertLayout), P, U64, I32, I32, I32, P, P, P, P, I32, P, P, P, P, P]),
     "tsx_moe_router_topk": (I32, [P, P, P, I32, I32, I32, P]),
     "tsx_moe_group": (I32, [P, I32, I32, I32, P, U64, P, P, P, P, P, P]),
     "tsx_moe_route_sort": (I32, [P, I32, I32, I32, P, P, P, P, P, P]),

@@ -26,6 +26,7 @@ SOURCES = [
     "tsx_weights.cpp",
     "strata_kernels.hip",
     "tsx_decode.hip",
+    "tsx_layer.hip",
     "tsx_route.hip",
     "tsx_prefill.hip",
 ]

@@ -58,7 +58,7 @@ __device__ __forceinline__ void row_dots(const uint8_t* __restrict__ row, const 
     for (int c = 0; c < NC; ++c) acc[c] = 0.f;
     for (int u = l; u < nu; u += LPR) {
         Unit w;
-        unit_load<T>(row, u, w);
+        unit_load<T>(row, u, w, grid_const());
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             if (c < n) {
@@ -177,7 +177,7 @@ __global__ void __launch_bounds__(kThreads) subblock_sums_kernel(const uint8_t* 
     const int64_t r = i / nu;
     const int u = (int) (i % nu);
     Unit wu;
-    unit_load<T>(w + (uint64_t) r * row_bytes, u, wu);
+    unit_load<T>(w + (uint64_t) r * row_bytes, u, wu, grid_const());
     for (int64_t c = 0; c < ncols; ++c) {
         Act a;
         act_load(x + c * nu + u, a);

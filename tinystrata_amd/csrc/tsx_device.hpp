@@ -14,6 +14,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cfloat>
 #include <cstdint>
 
 #include "tsx_moe.h"
@@ -22,18 +23,109 @@ namespace tsx {
 
 constexpr int kWave = 64;
 
-// ------------------------------------------------------------------ codebooks, expanded at compile time
+// 16 bytes as one vector: what the 128-bit global and LDS loads move
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ codebooks and sign tables, built at compile time
+// A sign entry turns 8 signs into what negates the matching bytes of two grid words: w = (g ^ mask) + one, with
+// mask = 0xFF and one = 0x01 in every negated byte (no carry crosses a byte: every grid byte is > 0).
+// xxs_sign is indexed by IQ3_XXS's 7-bit sign field (the 8th sign is the parity of the 7: ksigns_iq2xs),
+// s_sign by IQ3_S's sign byte.  Entry = {mask of values 0-3, mask of values 4-7, one 0-3, one 4-7}.
+struct SignEntry {
+    uint32_t mask_lo, mask_hi, one_lo, one_hi;
+};
 struct GridTables {
     uint32_t xxs[256];
     uint32_t s[512];
+    SignEntry xxs_sign[128];
+    SignEntry s_sign[256];
 };
+constexpr uint32_t spread_nibble(uint32_t nib) {  // bit i -> byte i = 1
+    return (nib & 1u) | (nib & 2u) << 7 | (nib & 4u) << 14 | (nib & 8u) << 21;
+}
+constexpr SignEntry sign_entry(uint32_t s8) {
+    const uint32_t lo = spread_nibble(s8 & 15u), hi = spread_nibble(s8 >> 4);
+    return SignEntry{lo * 0xFFu, hi * 0xFFu, lo, hi};
+}
+constexpr uint32_t parity7(uint32_t v) {
+    uint32_t p = 0;
+    for (int b = 0; b < 7; ++b) p ^= (v >> b) & 1u;
+    return p;
+}
 constexpr GridTables make_grid_tables() {
     GridTables g{};
     for (int i = 0; i < 256; ++i) g.xxs[i] = tsx_iq3xxs_word(i);
     for (int i = 0; i < 512; ++i) g.s[i] = tsx_iq3s_word(i);
+    for (uint32_t v = 0; v < 128; ++v) g.xxs_sign[v] = sign_entry(v | parity7(v) << 7);
+    for (uint32_t b = 0; b < 256; ++b) g.s_sign[b] = sign_entry(b);
     return g;
 }
 static __constant__ const GridTables kGrid = make_grid_tables();
+
+// where a kernel reads the tables from: the constant tables, or a copy in LDS
+struct GridRef {
+    const uint32_t* xxs;
+    const uint32_t* s;
+    const SignEntry* xxs_sign;
+    const SignEntry* s_sign;
+};
+__device__ __forceinline__ GridRef grid_const() { return GridRef{kGrid.xxs, kGrid.s, kGrid.xxs_sign, kGrid.s_sign}; }
+// LDS words the tables of weight type T take (0 for types without a codebook)
+template <int T>
+constexpr int grid_lds_words() {
+    return T == TSX_IQ3_XXS ? 256 + 4 * 128 : T == TSX_IQ3_S ? 512 + 4 * 256 : 0;
+}
+// the words of T's tables this thread copies (up to PER of them; word i = tid + n * k), loaded from the constant
+// tables: issue early, store later with grid_store
+template <int T, int PER>
+__device__ __forceinline__ void grid_fetch(uint32_t (&w)[PER], int tid, int n) {
+    constexpr int W = grid_lds_words<T>();
+    const uint32_t* src = T == TSX_IQ3_XXS ? kGrid.xxs : kGrid.s;
+    const uint32_t* sgn = (const uint32_t*) (T == TSX_IQ3_XXS ? kGrid.xxs_sign : kGrid.s_sign);
+    constexpr int G = T == TSX_IQ3_XXS ? 256 : 512;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {  // unconditional (clamped) loads keep the wait counts exact
+        const int i = min(tid + n * k, W - 1);
+        w[k] = i < G ? src[i] : sgn[i - G];
+    }
+}
+template <int T, int PER>
+__device__ __forceinline__ GridRef grid_store(uint32_t* lds, const uint32_t (&w)[PER], int tid, int n) {
+    constexpr int W = grid_lds_words<T>();
+    constexpr int G = T == TSX_IQ3_XXS ? 256 : 512;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int i = tid + n * k;
+        if (i < W) lds[i] = w[k];
+    }
+    GridRef r = grid_const();
+    if (T == TSX_IQ3_XXS) {
+        r.xxs = lds;
+        r.xxs_sign = (const SignEntry*) (lds + G);
+    } else if (T == TSX_IQ3_S) {
+        r.s = lds;
+        r.s_sign = (const SignEntry*) (lds + G);
+    }
+    return r;
+}
+// copies T's tables into LDS with the block's threads; the caller synchronizes before use
+template <int T>
+__device__ __forceinline__ GridRef grid_to_lds(uint32_t* lds, int tid, int n) {
+    constexpr int W = grid_lds_words<T>();
+    constexpr int G = T == TSX_IQ3_XXS ? 256 : 512;
+    const uint32_t* src = T == TSX_IQ3_XXS ? kGrid.xxs : kGrid.s;
+    const uint32_t* sgn = (const uint32_t*) (T == TSX_IQ3_XXS ? kGrid.xxs_sign : kGrid.s_sign);
+    for (int i = tid; i < W; i += n) lds[i] = i < G ? src[i] : sgn[i - G];
+    GridRef r = grid_const();
+    if (T == TSX_IQ3_XXS) {
+        r.xxs = lds;
+        r.xxs_sign = (const SignEntry*) (lds + G);
+    } else if (T == TSX_IQ3_S) {
+        r.s = lds;
+        r.s_sign = (const SignEntry*) (lds + G);
+    }
+    return r;
+}
 
 // ------------------------------------------------------------------ scalar helpers
 __device__ __forceinline__ float h2f(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
@@ -49,13 +141,6 @@ __device__ __forceinline__ uint32_t ld32a2(const uint8_t* p) {
 }
 __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*) p; }
 
-// the 4 bytes of a grid word negated where the nibble's bits are set: (g ^ 0xFF) + 1 per byte (no carry: g > 0)
-__device__ __forceinline__ int signed4(uint32_t g, uint32_t nib) {
-    const uint32_t one = (nib * 0x204081u) & 0x01010101u;  // bit i of nib -> byte i = 1
-    return (int) ((g ^ (one * 0xFFu)) + one);
-}
-// ksigns_iq2xs: 7 sign bits plus an even-parity bit 7
-__device__ __forceinline__ uint32_t ksign8(uint32_t v7) { return v7 | ((uint32_t) __builtin_popcount(v7) & 1u) << 7; }
 
 // ------------------------------------------------------------------ unit decode
 struct Unit {
@@ -69,9 +154,9 @@ template <> struct Fmt<TSX_IQ3_S> { static constexpr int upb = 8, bytes = 110; }
 template <> struct Fmt<TSX_Q4_K> { static constexpr int upb = 8, bytes = 144; };
 template <> struct Fmt<TSX_Q8_0> { static constexpr int upb = 1, bytes = 34; };
 
-template <int T> __device__ __forceinline__ void unit_load(const uint8_t* row, int u, Unit& o);
+template <int T> __device__ __forceinline__ void unit_load(const uint8_t* row, int u, Unit& o, GridRef g);
 
-template <> __device__ __forceinline__ void unit_load<TSX_IQ3_XXS>(const uint8_t* row, int u, Unit& o) {
+template <> __device__ __forceinline__ void unit_load<TSX_IQ3_XXS>(const uint8_t* row, int u, Unit& o, GridRef g) {
     const uint8_t* blk = row + (u >> 3) * 98;
     const int j = u & 7;
     const float d = h2f((uint16_t) ld16(blk));
@@ -79,35 +164,39 @@ template <> __device__ __forceinline__ void unit_load<TSX_IQ3_XXS>(const uint8_t
     const uint32_t aux = ld32a2(blk + 66 + 4 * j);
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-        const uint32_t s = ksign8((aux >> (7 * l)) & 127u);
+        const SignEntry sg = g.xxs_sign[(aux >> (7 * l)) & 127u];
         const uint32_t q = l < 2 ? q0 : q1;
         const uint32_t i0 = (q >> (16 * (l & 1))) & 255u, i1 = (q >> (16 * (l & 1) + 8)) & 255u;
-        o.w[2 * l] = signed4(kGrid.xxs[i0], s & 15u);
-        o.w[2 * l + 1] = signed4(kGrid.xxs[i1], s >> 4);
+        o.w[2 * l] = (int) ((g.xxs[i0] ^ sg.mask_lo) + sg.one_lo);
+        o.w[2 * l + 1] = (int) ((g.xxs[i1] ^ sg.mask_hi) + sg.one_hi);
     }
     o.a = d * 0.25f * (float) (2 * (int) (aux >> 28) + 1);
     o.b = 0.f;
 }
 
-template <> __device__ __forceinline__ void unit_load<TSX_IQ3_S>(const uint8_t* row, int u, Unit& o) {
+template <> __device__ __forceinline__ void unit_load<TSX_IQ3_S>(const uint8_t* row, int u, Unit& o, GridRef g) {
     const uint8_t* blk = row + (u >> 3) * 110;
     const int j = u & 7;
     const float d = h2f((uint16_t) ld16(blk));
     const uint32_t q0 = ld32a2(blk + 2 + 8 * j), q1 = ld32a2(blk + 6 + 8 * j);
     const uint32_t qh = blk[66 + j];
-    const uint32_t sg = ld32a2(blk + 74 + 4 * j);
+    const uint32_t sb = ld32a2(blk + 74 + 4 * j);
     const uint32_t sc = (blk[106 + (j >> 1)] >> (4 * (j & 1))) & 15u;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t q = k < 4 ? q0 : q1;
-        const uint32_t idx = ((q >> (8 * (k & 3))) & 255u) | (((qh >> k) & 1u) << 8);
-        o.w[k] = signed4(kGrid.s[idx], (sg >> (4 * k)) & 15u);
+    for (int l = 0; l < 4; ++l) {
+        const SignEntry sg = g.s_sign[(sb >> (8 * l)) & 255u];
+        const uint32_t q = l < 2 ? q0 : q1;
+        const int k0 = 2 * l, k1 = 2 * l + 1;
+        const uint32_t i0 = ((q >> (8 * (k0 & 3))) & 255u) | (((qh >> k0) & 1u) << 8);
+        const uint32_t i1 = ((q >> (8 * (k1 & 3))) & 255u) | (((qh >> k1) & 1u) << 8);
+        o.w[k0] = (int) ((g.s[i0] ^ sg.mask_lo) + sg.one_lo);
+        o.w[k1] = (int) ((g.s[i1] ^ sg.mask_hi) + sg.one_hi);
     }
     o.a = d * (float) (2 * (int) sc + 1);
     o.b = 0.f;
 }
 
-template <> __device__ __forceinline__ void unit_load<TSX_Q4_K>(const uint8_t* row, int u, Unit& o) {
+template <> __device__ __forceinline__ void unit_load<TSX_Q4_K>(const uint8_t* row, int u, Unit& o, GridRef g) {
     const uint8_t* blk = row + (u >> 3) * 144;
     const int j = u & 7;
     const float d = h2f((uint16_t) ld16(blk)), dmin = h2f((uint16_t) ld16(blk + 2));
@@ -128,7 +217,7 @@ template <> __device__ __forceinline__ void unit_load<TSX_Q4_K>(const uint8_t* r
     o.b = dmin * (float) m;
 }
 
-template <> __device__ __forceinline__ void unit_load<TSX_Q8_0>(const uint8_t* row, int u, Unit& o) {
+template <> __device__ __forceinline__ void unit_load<TSX_Q8_0>(const uint8_t* row, int u, Unit& o, GridRef g) {
     const uint8_t* blk = row + u * 34;
     const float d = h2f((uint16_t) ld16(blk));
 #pragma unroll
@@ -176,6 +265,106 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// ------------------------------------------------------------------ DPP reductions (no LDS round trips)
+// Four DPP steps reduce each 16-lane row (xor 1, xor 2, then the half-row and row mirrors); the row totals are then
+// combined from lanes 15, 31, 47 and 63 with readlane.  Every lane of the span ends with the same bits (each DPP step
+// combines a value with its partner symmetrically, and the last step hands every lane one scalar).  For spans of 32
+// or 64 lanes all 64 lanes must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_of(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+template <typename Op>
+__device__ __forceinline__ float row_reduce16(float v, Op op) {
+    v = op(v, dpp_mov<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = op(v, dpp_mov<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = op(v, dpp_mov<0x141>(v));  // row_half_mirror
+    v = op(v, dpp_mov<0x140>(v));  // row_mirror
+    return v;
+}
+// over each half wave (lanes 0-31, 32-63)
+template <typename Op>
+__device__ __forceinline__ float reduce32(float v, Op op) {
+    v = row_reduce16(v, op);
+    const float lo = op(lane_of(v, 15), lane_of(v, 31)), hi = op(lane_of(v, 47), lane_of(v, 63));
+    return (__lane_id() < 32) ? lo : hi;
+}
+// over the wave
+template <typename Op>
+__device__ __forceinline__ float reduce64(float v, Op op) {
+    v = row_reduce16(v, op);
+    return op(op(lane_of(v, 15), lane_of(v, 31)), op(lane_of(v, 47), lane_of(v, 63)));
+}
+struct OpAddF {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+// op over aligned groups of W consecutive lanes (W = 2, 4, 8, 16, 32 or 64), every lane of a group ending with the
+// result
+template <int W, typename Op>
+__device__ __forceinline__ float lanes_reduce(float v, Op op) {
+    static_assert(W == 2 || W == 4 || W == 8 || W == 16 || W == 32 || W == 64, "lanes_reduce width");
+    if constexpr (W == 32) {
+        return reduce32(v, op);
+    } else if constexpr (W == 64) {
+        return reduce64(v, op);
+    } else {
+        v = op(v, dpp_mov<0xB1>(v));
+        if constexpr (W >= 4) v = op(v, dpp_mov<0x4E>(v));
+        if constexpr (W >= 8) v = op(v, dpp_mov<0x141>(v));
+        if constexpr (W >= 16) v = op(v, dpp_mov<0x140>(v));
+        return v;
+    }
+}
+template <int W>
+__device__ __forceinline__ float lanes_sum(float v) {
+    return lanes_reduce<W>(v, OpAddF());
+}
+
+// ------------------------------------------------------------------ wave argmax on (value, id) keys
+// A float's order as an unsigned word (larger float -> larger word; -inf below -FLT_MAX below every probability).
+__device__ __forceinline__ uint32_t ord_key(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+// (hi, lo) is the larger 64-bit key of the pair: hi = ord_key(value), lo = ~id (ties go to the lower id)
+__device__ __forceinline__ void key_max(uint32_t& hi, uint32_t& lo, uint32_t oh, uint32_t ol) {
+    const bool take = oh > hi || (oh == hi && ol > lo);
+    hi = take ? oh : hi;
+    lo = take ? ol : lo;
+}
+template <int CTRL>
+__device__ __forceinline__ void key_step(uint32_t& hi, uint32_t& lo) {
+    const uint32_t oh = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) hi, CTRL, 0xF, 0xF, false);
+    const uint32_t ol = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) lo, CTRL, 0xF, 0xF, false);
+    key_max(hi, lo, oh, ol);
+}
+// the wave's largest key, the same in every lane (all 64 lanes active)
+__device__ __forceinline__ void wave_key_max(uint32_t& hi, uint32_t& lo) {
+    key_step<0xB1>(hi, lo);
+    key_step<0x4E>(hi, lo);
+    key_step<0x141>(hi, lo);
+    key_step<0x140>(hi, lo);
+    uint32_t h = (uint32_t) __builtin_amdgcn_readlane((int) hi, 15), l = (uint32_t) __builtin_amdgcn_readlane((int) lo, 15);
+    key_max(h, l, (uint32_t) __builtin_amdgcn_readlane((int) hi, 31), (uint32_t) __builtin_amdgcn_readlane((int) lo, 31));
+    key_max(h, l, (uint32_t) __builtin_amdgcn_readlane((int) hi, 47), (uint32_t) __builtin_amdgcn_readlane((int) lo, 47));
+    key_max(h, l, (uint32_t) __builtin_amdgcn_readlane((int) hi, 63), (uint32_t) __builtin_amdgcn_readlane((int) lo, 63));
+    hi = h;
+    lo = l;
+}
+
+struct OpMax {
+    __device__ float operator()(float a, float b) const { return __builtin_fmaxf(a, b); }
+};
+struct OpAdd {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+
 // ------------------------------------------------------------------ Q8_1 of 32 values held by 32 lanes
 // lane i (i = lane & 31) holds x; the 32-lane xor tree for amax and for the sum (the order the oracle restates)
 __device__ __forceinline__ float q8_1_finite(float v) { return fabsf(v) > 65504.0f ? copysignf(65504.0f, v) : v; }
@@ -196,6 +385,69 @@ __device__ __forceinline__ void q8_1_store32(float x, tsx_block_q8_1* y, int i) 
     if (i == 0) {
         y->d = f2h(q8_1_finite(d));
         y->s = f2h(q8_1_finite(sum));
+    }
+}
+
+
+// ------------------------------------------------------------------ routing of one token by one wave
+// Reference route_topk<NE,K> (src/kernels/cuda/native_router.cu:42-95): softmax with the max subtracted and one
+// reciprocal of the sum, NaN probabilities as -FLT_MAX, k rounds of argmax (ties to the lower id), weights divided by
+// max(sum of the picks, 6.1035e-5).  Expert e = lane + 64 i; n_expert a multiple of 64 up to kMaxExperts.  Each round
+// is one wave argmax on (probability, id) keys by DPP; the picked expert's key drops below every other.
+// ids / wts may point to global memory or LDS; every lane of the wave must call.
+constexpr int kMaxExperts = 512;
+__device__ __forceinline__ void route_token(const float* __restrict__ l, int n_expert, int k, int lane, int32_t* ids,
+                                            float* wts) {
+    constexpr int VM = kMaxExperts / 64;
+    const int V = n_expert / 64;
+    float v[VM];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VM; ++i) {  // unconditional (clamped) loads keep the wait counts exact
+        const float li = l[lane + 64 * min(i, V - 1)];
+        v[i] = i < V ? li : -INFINITY;
+        mx = __builtin_fmaxf(mx, v[i]);
+    }
+    mx = reduce64(mx, OpMax());
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < VM; ++i) {
+        v[i] = i < V ? expf(v[i] - mx) : 0.f;
+        sum += v[i];
+    }
+    const float rcp = 1.0f / reduce64(sum, OpAddF());
+    uint32_t key[VM];
+#pragma unroll
+    for (int i = 0; i < VM; ++i) {
+        float p = v[i] * rcp;
+        if (__builtin_isnan(p)) p = -FLT_MAX;
+        key[i] = i < V ? ord_key(p) : 0u;  // 0: below every probability, -inf included
+    }
+    float sel_sum = 0.f, my_p = 0.f;
+    int my_id = 0;
+    for (int r = 0; r < k; ++r) {
+        uint32_t hi = key[0], lo = ~(uint32_t) lane;
+#pragma unroll
+        for (int i = 1; i < VM; ++i)
+            if (i < V) key_max(hi, lo, key[i], ~(uint32_t) (lane + 64 * i));
+        wave_key_max(hi, lo);
+        const int x = (int) ~lo;
+        const float p = key_value(hi);
+        if ((x & 63) == lane) {
+#pragma unroll
+            for (int i = 0; i < VM; ++i)
+                if (i == (x >> 6)) key[i] = 0u;
+        }
+        sel_sum += p;
+        if (lane == r) {
+            my_id = x;
+            my_p = p;
+        }
+    }
+    const float inv = 1.0f / __builtin_fmaxf(sel_sum, 6.103515625e-5f);
+    if (lane < k) {
+        ids[lane] = my_id;
+        wts[lane] = my_p * inv;
     }
 }
 

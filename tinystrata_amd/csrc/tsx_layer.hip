@@ -1,0 +1,565 @@
+// tsx_layer.hip - a whole decode MoE layer (1..8 tokens) in two launches on gfx950.
+//
+// Reference: the MoE block of src/qwen35/q36_engine.cu:2821-2925 - k_route_group (src/qwen35/q36_kernels.cuh:383-474),
+// native_expert_grouped (src/kernels/cuda/iq_kernels.cu:2835-2982), the shared expert (mmvq, SwiGLU + Q8_1, mmvq:
+// q36_engine.cu:2906-2913) and k_moe_out_small without the norm (q36_kernels.cuh:248-290).  The reference spends
+// five to eight launches per layer on that sequence; here it is two, with nothing between them on the host.
+//
+// At one token the layer is bound by latency and by the vector ALU, not by HBM: 11.3 MB is 1.4 us of HBM time, a
+// dependent global round trip costs about a microsecond, and decoding the IQ3 codebooks costs ~100 VALU operations
+// per 32 weights - about 2 us of the whole chip's vector issue for one token-layer.  So the work is cut fine enough
+// to reach every CU, each launch keeps its chain of dependent memory accesses short (A: logits -> routing ->
+// weights; B: one table read -> weights) and issues everything else alongside, and cross-lane reductions use DPP
+// and readlane rather than LDS permutes.
+//
+// Launch A, grid (n_ff/32 slices, cap_groups [+1 for the shared expert]), 1024 threads.  Every block
+//   1. routes every token (route_token: one wave per token, the code of tsx_moe_router_topk) and groups the entries
+//      by expert in LDS (ascending id, entries in entry order); it takes group blockIdx.y, or the shared expert in
+//      the last block row;
+//   2. issues 16-byte loads of the slice's 32 gate rows and 32 up rows (contiguous in the blob; rows too long for
+//      one 64 KB LDS slab come in chunks, the next chunk's loads issued before the current one is computed), with
+//      the activations and codebooks requested at the start, and quantizes the activations to Q8_1 in LDS while
+//      the rows arrive;
+//   3. dots the rows with every entry (each unit decoded once for all entries), applies SwiGLU (the product rounded
+//      on its own) and writes the slice's Q8_1 block of h per entry.  Block (0, 0) also writes ids / wts and the
+//      tables launch B needs.
+// Launch B, grid n_embd/8, 256 threads.  Every block owns 8 output rows: it reads the tables and every entry's h in
+//   one round trip, loads those 8 rows of every used expert's down matrix (and the shared expert's) into LDS,
+//   dots, and combines in pick order: y += w0*p0, fmaf(wj, pj, .) ..., + sigmoid(sgate)*shared -
+//   tsx_moe_combine's arithmetic.
+//
+// Every load a block can issue before it needs the data is issued unconditionally (indices clamped into range),
+// so the compiler's wait counts stay exact and the loads stay in flight together.
+//
+// Memory per layer at config 2 (N 2048, FF 512, IQ3_XXS gate/up, IQ3_S down, 8 routed + 1 shared expert): launch A
+// reads 9 x 802,816 B of gate/up rows in 144 blocks of 50 KB; launch B 9 x 450,560 B of down rows in 256 blocks of
+// 15.8 KB.
+#include "tsx_common.hpp"
+#include "tsx_device.hpp"
+
+#include <climits>
+
+namespace tsx {
+namespace {
+
+constexpr int kMaxTok = 8;            // tokens per decode layer call
+constexpr int kMaxEnt = 64;           // routed entries (tokens x k)
+constexpr int kNC = 4;                // entries per pass over a row's units
+constexpr int kThreadsA = 1024;
+constexpr int kSliceA = 32;           // gate (and up) rows per block of launch A: one Q8_1 block of h per entry
+constexpr int kSlabA = 64 * 1024;     // LDS bytes of a chunk of gate + up rows
+constexpr int kLoadsA = kSlabA / 16 / kThreadsA;
+constexpr int kXLoads = 2;            // activation quads per thread per round of launch A
+constexpr int kThreadsB = 256;
+constexpr int kRowsB = 8;             // output rows per block of launch B
+constexpr int kSlabB = 48 * 1024;     // LDS bytes of down rows per group chunk
+constexpr int kLoadsB = kSlabB / 16 / kThreadsB;
+constexpr int kHLoads = 12;           // 16-byte pieces of h per thread per round of launch B
+constexpr int kTprB = 2;              // threads per (group, row) pair in launch B
+static_assert(kMaxTok <= kThreadsA / 64, "one wave per token in the routing");
+
+// the tables launch A leaves for launch B, at the start of the scratch buffer
+struct LayerTables {
+    int32_t n_groups;
+    int32_t pad[3];
+    int32_t grp_expert[kMaxEnt];
+    int32_t grp_start[kMaxEnt + 4];
+    int32_t ent_pos[kMaxEnt];     // entry e = t*k + j -> its position in expert order
+    float wts[kMaxEnt];
+};
+constexpr int kTableWords = sizeof(LayerTables) / 4;
+static_assert(kTableWords <= 2 * kThreadsB, "launch B reads the tables in two rounds");
+constexpr size_t kTablesBytes = (sizeof(LayerTables) + 255) & ~(size_t) 255;
+
+struct LayerArgs {
+    tsx_expert_layout L;
+    const uint8_t* blobs;
+    uint64_t stride;
+    int n_expert, k, n_tok, cap_groups;
+    const float* logits;
+    const float* x;
+    const uint8_t* shared;
+    const float* sgate;
+    int sg_stride;
+    int rows_c;                   // gate (and up) rows per chunk of launch A: 32, 16 or 8
+    float* y;
+    int32_t* ids;
+    float* wts;
+    LayerTables* tab;
+    int8_t* hc;                   // Q8_1 codes of h [P][n_ff], P = n_tok * k (+ n_tok shared): expert order positions
+    float* hd;                    // their scales [P][n_ff / 32], right after the codes
+};
+
+// one Q8_1 activation unit (32 codes + scale) from LDS planes (codes row-major, one float scale per 32)
+__device__ __forceinline__ void act_planes(const int8_t* codes, const float* d, Act& a) {
+    const v4i* p = (const v4i*) codes;
+    const v4i q0 = p[0], q1 = p[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a.q[i] = q0[i];
+        a.q[4 + i] = q1[i];
+    }
+    a.d = *d;
+}
+
+// the Q8_1 code of v in a block whose largest magnitude is amax (scale d = q8_1_finite(amax / 127)): the codes of
+// q8_1_store32, byte for byte
+__device__ __forceinline__ int q8_1_code(float v, float amax, float d) {
+    if (amax == 0.0f) return 0;
+    const float r = roundf(v / d);
+    return (int) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
+}
+
+// Q8_1 of a 32-value block held as 4 floats by each of 8 consecutive lanes (lane l of the block: values 4l..4l+3)
+// into LDS planes.  All 64 lanes of the wave take part.
+__device__ __forceinline__ void q8_1_quad_to_lds(const float4& x, bool valid, int8_t* codes, float* d, int l8) {
+    float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+    amax = lanes_reduce<8>(amax, OpMax());
+    const float dd = q8_1_finite(amax / 127.0f);
+    const uint32_t packed = ((uint32_t) q8_1_code(x.x, amax, dd) & 0xFFu) | ((uint32_t) q8_1_code(x.y, amax, dd) & 0xFFu) << 8 |
+                            ((uint32_t) q8_1_code(x.z, amax, dd) & 0xFFu) << 16 | ((uint32_t) q8_1_code(x.w, amax, dd) & 0xFFu) << 24;
+    if (valid) {
+        *(uint32_t*) codes = packed;
+        if (l8 == 0) *d = h2f(f2h(dd));
+    }
+}
+
+template <int W>
+__device__ __forceinline__ void sum_acc(float (&acc)[kNC]) {
+#pragma unroll
+    for (int c = 0; c < kNC; ++c) acc[c] = lanes_sum<W>(acc[c]);
+}
+
+// ------------------------------------------------------------------ launch A
+template <int GT>
+__global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
+#pragma clang fp contract(off)
+    constexpr int GW = (grid_lds_words<GT>() + kThreadsA - 1) / kThreadsA;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ __attribute__((aligned(16))) uint32_t s_grid[GW > 0 ? GW * kThreadsA : 4];
+    __shared__ int32_t s_ids[kMaxEnt], s_sorted[kMaxEnt], s_pos_ent[kMaxEnt], s_ent_pos[kMaxEnt];
+    __shared__ int32_t s_grp_expert[kMaxEnt], s_grp_start[kMaxEnt + 1];
+    __shared__ float s_wts[kMaxEnt];
+    __shared__ int s_ngroups;
+    __shared__ float s_gu[kMaxTok][2 * kSliceA];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int T = a.n_tok, k = a.k, n_ent = T * k;
+    const tsx_expert_layout L = a.L;
+    const int N = (int) L.n_embd, NU = N / 32, FF = (int) L.n_ff;
+
+    // 0. what does not depend on the routing is requested first: the codebooks and, when they fit in registers,
+    //    every token's activations
+    uint32_t gw[GW > 0 ? GW : 1];
+    if constexpr (GW > 0) grid_fetch<GT, GW>(gw, tid, kThreadsA);
+    const int nq_all = T * N / 4;
+    const bool x_early = nq_all <= kThreadsA * kXLoads;
+    float4 xv[kXLoads];
+    if (x_early) {
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) xv[i] = ((const float4*) a.x)[min(tid + kThreadsA * i, nq_all - 1)];
+    }
+
+    // 1. routing (one wave per token) and grouping, identical in every block
+    if (wave < T) route_token(a.logits + (int64_t) wave * a.n_expert, a.n_expert, k, lane, s_ids + wave * k, s_wts + wave * k);
+    __syncthreads();
+    if (wave == 0) {  // rank of entry `lane` in (expert, entry) order
+        const int e = lane;
+        const int key = e < n_ent ? s_ids[e] * 64 + e : INT_MAX;
+        int rank = 0;
+        for (int i = 0; i < n_ent; ++i) rank += __builtin_amdgcn_readlane(key, i) < key;
+        if (e < n_ent) {
+            s_sorted[rank] = s_ids[e];
+            s_pos_ent[rank] = e;
+            s_ent_pos[e] = rank;
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {  // a group starts where the expert changes
+        const int p = lane;
+        const int xp = p < n_ent ? s_sorted[p] : -1;
+        const bool start = p < n_ent && (p == 0 || s_sorted[p - 1] != xp);
+        const uint64_t mask = __ballot(start);
+        if (start) {
+            const int g = __builtin_popcountll(mask & (~0ull >> (63 - p))) - 1;
+            s_grp_expert[g] = xp;
+            s_grp_start[g] = p;
+        }
+        if (lane == 0) {
+            const int ng = __builtin_popcountll(mask);
+            s_ngroups = ng;
+            s_grp_start[ng] = n_ent;
+        }
+    }
+    __syncthreads();
+    const int ng = s_ngroups;
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        if (tid < n_ent) {
+            a.ids[tid] = s_ids[tid];
+            a.wts[tid] = s_wts[tid];
+            a.tab->wts[tid] = s_wts[tid];
+            a.tab->ent_pos[tid] = s_ent_pos[tid];
+        }
+        if (tid <= ng) {
+            if (tid < ng) a.tab->grp_expert[tid] = s_grp_expert[tid];
+            a.tab->grp_start[tid] = s_grp_start[tid];
+        }
+        if (tid == 0) a.tab->n_groups = ng;
+    }
+
+    // this block's expert and entries
+    const int gy = blockIdx.y;
+    const bool is_shared = gy == a.cap_groups;
+    if (!is_shared && gy >= ng) return;  // the whole block: no group this far
+    const uint8_t* blob = is_shared ? a.shared : a.blobs + (uint64_t) s_grp_expert[gy] * a.stride;
+    const int p0 = is_shared ? n_ent : s_grp_start[gy];
+    const int n_e = is_shared ? T : s_grp_start[gy + 1] - p0;  // <= T: a token picks an expert once
+
+    // 2. the first chunk's rows in flight, then the activations
+    const int rows_c = a.rows_c, nchunks = kSliceA / rows_c;
+    const uint64_t gu_row = L.gu_row;
+    const int n16 = (int) (rows_c * gu_row / 16);  // 16-byte pieces of a chunk's gate (or up) rows
+    const int j = blockIdx.x;                      // slice: rows [32 j, 32 j + 32)
+    v4i reg[kLoadsA];
+    auto issue = [&](int c) {
+        const uint64_t off = (uint64_t) (kSliceA * j + c * rows_c) * gu_row;
+        const v4i* gsrc = (const v4i*) (blob + off);
+        const v4i* usrc = (const v4i*) (blob + L.up_off + off);
+#pragma unroll
+        for (int i = 0; i < kLoadsA; ++i) {  // unconditional (clamped) loads keep the wait counts exact
+            const int idx = min(tid + kThreadsA * i, 2 * n16 - 1);
+            reg[i] = __builtin_nontemporal_load(idx < n16 ? gsrc + idx : usrc + (idx - n16));
+        }
+    };
+    v4i* slab = (v4i*) smem;
+    auto store = [&]() {
+#pragma unroll
+        for (int i = 0; i < kLoadsA; ++i) {
+            const int idx = tid + kThreadsA * i;
+            if (idx < 2 * n16) slab[idx] = reg[i];
+        }
+    };
+    issue(0);
+
+    // Q8_1 planes of the activations: every token's (row t) when they were prefetched, else the block's entries'
+    // tokens (row c = entry p0 + c)
+    int8_t* s_xq = (int8_t*) (smem + kSlabA);
+    float* s_xd = (float*) (s_xq + T * N);
+    if (x_early) {
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i)
+            if (kThreadsA * i < nq_all)  // the same for every thread of the block
+                q8_1_quad_to_lds(xv[i], tid + kThreadsA * i < nq_all, s_xq + 4 * (tid + kThreadsA * i),
+                                 s_xd + (tid + kThreadsA * i) / 8, tid & 7);
+    } else {
+        const int nq = n_e * N / 4;  // quads of activation values; 8 consecutive lanes hold one Q8_1 block
+        for (int base = 0; base < nq; base += kThreadsA * kXLoads) {
+#pragma unroll
+            for (int i = 0; i < kXLoads; ++i) {
+                const int qc = min(base + tid + kThreadsA * i, nq - 1);
+                const int c = (4 * qc) / N, col = 4 * qc - c * N;
+                const int t = is_shared ? c : s_pos_ent[p0 + c] / k;
+                xv[i] = *(const float4*) (a.x + (int64_t) t * N + col);
+            }
+#pragma unroll
+            for (int i = 0; i < kXLoads; ++i) {
+                const int qd = base + tid + kThreadsA * i;
+                if (base + kThreadsA * i < nq) q8_1_quad_to_lds(xv[i], qd < nq, s_xq + 4 * qd, s_xd + qd / 8, tid & 7);
+            }
+        }
+    }
+    auto x_row = [&](int c) { return x_early ? (is_shared ? c : s_pos_ent[p0 + c] / k) : c; };
+    GridRef grid = grid_const();
+    if constexpr (GW > 0) grid = grid_store<GT, GW>(s_grid, gw, tid, kThreadsA);
+
+    // 3. each chunk's rows against every entry: 2 * rows_c rows (gate, then up), tpr lanes per row
+    const int tpr = kThreadsA / (2 * rows_c);
+    const int rr = tid / tpr, l = tid % tpr;
+    for (int c = 0; c < nchunks; ++c) {
+        if (c > 0) __syncthreads();  // the previous chunk's rows are consumed
+        store();
+        __syncthreads();
+        if (c + 1 < nchunks) issue(c + 1);
+        const uint8_t* row = (const uint8_t*) slab + (uint64_t) rr * gu_row;
+        for (int e0 = 0; e0 < n_e; e0 += kNC) {
+            const int n = min(kNC, n_e - e0);
+            float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
+            for (int u = l; u < NU; u += tpr) {
+                Unit w;
+                unit_load<GT>(row, u, w, grid);
+#pragma unroll
+                for (int cc = 0; cc < kNC; ++cc) {
+                    if (cc < n) {
+                        Act xa;
+                        const int xr = x_row(e0 + cc);
+                        act_planes(s_xq + xr * N + 32 * u, s_xd + xr * NU + u, xa);
+                        int S, M;
+                        acc[cc] += unit_dot<GT>(w, xa, S, M);
+                    }
+                }
+            }
+            switch (tpr) {  // the tpr lanes of a row are consecutive and tpr divides 64
+                case 16: sum_acc<16>(acc); break;
+                case 32: sum_acc<32>(acc); break;
+                default: sum_acc<64>(acc); break;
+            }
+            if (l == 0) {
+                const int col = rr < rows_c ? c * rows_c + rr : kSliceA + c * rows_c + (rr - rows_c);
+                for (int cc = 0; cc < n; ++cc) s_gu[e0 + cc][col] = acc[cc];
+            }
+        }
+    }
+    __syncthreads();
+
+    // h = silu(gate) * up and its Q8_1 block for each entry: 32-lane group c takes entry c (all lanes take part)
+    const int c = min(tid >> 5, kMaxTok - 1), i = tid & 31;
+    const float g = s_gu[c][i];
+    const float h = (g / (1.0f + expf(-g))) * s_gu[c][kSliceA + i];
+    const float amax = lanes_reduce<32>(fabsf(h), OpMax());
+    const float dd = q8_1_finite(amax / 127.0f);
+    if ((tid >> 5) < n_e) {
+        const int64_t p = p0 + c;
+        a.hc[p * FF + kSliceA * j + i] = (int8_t) q8_1_code(h, amax, dd);
+        if (i == 0) a.hd[p * (FF / 32) + j] = h2f(f2h(dd));
+    }
+}
+
+// ------------------------------------------------------------------ launch B
+template <int DT>
+__global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
+#pragma clang fp contract(off)
+    constexpr int GW = (grid_lds_words<DT>() + kThreadsB - 1) / kThreadsB;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ __attribute__((aligned(16))) uint32_t s_grid[GW > 0 ? GW * kThreadsB : 4];
+    __shared__ LayerTables s_tab;
+    __shared__ float s_part[kMaxEnt + kMaxTok][kRowsB];
+
+    const int tid = threadIdx.x;
+    const int T = a.n_tok, k = a.k, n_ent = T * k;
+    const tsx_expert_layout L = a.L;
+    const int N = (int) L.n_embd, FF = (int) L.n_ff, NUd = FF / 32;
+    const uint64_t d_row = L.d_row;
+    const int r0 = blockIdx.x * kRowsB;
+
+    // requested together: the codebooks, the tables and every entry's h (codes, then scales: contiguous in the
+    // scratch, as in LDS), whose positions are fixed: n_tok * k routed, then n_tok shared
+    uint32_t gw[GW > 0 ? GW : 1];
+    if constexpr (GW > 0) grid_fetch<DT, GW>(gw, tid, kThreadsB);
+    const int P = n_ent + (a.shared ? T : 0);
+    const int nh = (P * FF + P * NUd * 4) / 16;  // 16-byte pieces (n_ff is a multiple of 128)
+    const v4i* hsrc = (const v4i*) a.hc;
+    v4i hv[kHLoads];
+#pragma unroll
+    for (int i = 0; i < kHLoads; ++i) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
+    {
+        const uint32_t* src = (const uint32_t*) a.tab;
+        uint32_t* dst = (uint32_t*) &s_tab;
+        const uint32_t w0 = src[tid];
+        const uint32_t w1 = src[min(tid + kThreadsB, kTableWords - 1)];
+        if (tid < kTableWords) dst[tid] = w0;
+        if (tid + kThreadsB < kTableWords) dst[tid + kThreadsB] = w1;
+    }
+    __syncthreads();
+    const int ng = s_tab.n_groups;
+    const int G = ng + (a.shared ? 1 : 0);  // group ng is the shared expert: positions [n_ent, n_ent + T)
+    auto grp_blob = [&](int g) { return g < ng ? a.blobs + (uint64_t) s_tab.grp_expert[g] * a.stride : a.shared; };
+    auto grp_lo = [&](int g) { return g < ng ? s_tab.grp_start[g] : n_ent; };
+    auto grp_hi = [&](int g) { return g < ng ? s_tab.grp_start[g + 1] : n_ent + T; };
+
+    const int n16g = (int) (kRowsB * d_row / 16);  // 16-byte pieces of one group's 8 rows
+    const int gc = max(1, min(G, (kSlabB / 16) / n16g));
+    v4i reg[kLoadsB];
+    auto issue = [&](int g0) {
+        const int gn = min(gc, G - g0);
+#pragma unroll
+        for (int i = 0; i < kLoadsB; ++i) {  // unconditional (clamped) loads keep the wait counts exact
+            const int idx = min(tid + kThreadsB * i, gn * n16g - 1);
+            const int g = g0 + idx / n16g;
+            const v4i* src = (const v4i*) (grp_blob(g) + L.down_off + (uint64_t) r0 * d_row);
+            reg[i] = __builtin_nontemporal_load(src + idx % n16g);
+        }
+    };
+    v4i* slab = (v4i*) smem;
+    issue(0);
+
+    // h into LDS: the prefetched pieces, then any rest
+    int8_t* s_hq = (int8_t*) (smem + (size_t) gc * n16g * 16);
+    float* s_hd = (float*) (s_hq + (size_t) P * FF);
+    v4i* hdst = (v4i*) s_hq;
+#pragma unroll
+    for (int i = 0; i < kHLoads; ++i)
+        if (tid + kThreadsB * i < nh) hdst[tid + kThreadsB * i] = hv[i];
+    for (int idx = tid + kThreadsB * kHLoads; idx < nh; idx += kThreadsB) hdst[idx] = hsrc[idx];
+    GridRef grid = grid_const();
+    if constexpr (GW > 0) grid = grid_store<DT, GW>(s_grid, gw, tid, kThreadsB);
+
+    const int l = tid % kTprB;
+    for (int g0 = 0; g0 < G; g0 += gc) {
+        const int gn = min(gc, G - g0);
+        if (g0 > 0) __syncthreads();  // the previous chunk's rows are consumed
+#pragma unroll
+        for (int i = 0; i < kLoadsB; ++i) {
+            const int idx = tid + kThreadsB * i;
+            if (idx < gn * n16g) slab[idx] = reg[i];
+        }
+        __syncthreads();
+        if (g0 + gc < G) issue(g0 + gc);
+        for (int pair = tid / kTprB; pair < gn * kRowsB; pair += kThreadsB / kTprB) {
+            const int gl = pair / kRowsB, r = pair % kRowsB, g = g0 + gl;
+            const uint8_t* row = (const uint8_t*) slab + (uint64_t) pair * d_row;
+            const int q0 = grp_lo(g), q1 = grp_hi(g);
+            for (int e0 = q0; e0 < q1; e0 += kNC) {
+                const int n = min(kNC, q1 - e0);
+                float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
+                for (int u = l; u < NUd; u += kTprB) {
+                    Unit w;
+                    unit_load<DT>(row, u, w, grid);
+#pragma unroll
+                    for (int cc = 0; cc < kNC; ++cc) {
+                        if (cc < n) {
+                            Act xa;
+                            act_planes(s_hq + (size_t) (e0 + cc) * FF + 32 * u, s_hd + (e0 + cc) * NUd + u, xa);
+                            int S, M;
+                            acc[cc] += unit_dot<DT>(w, xa, S, M);
+                        }
+                    }
+                }
+                sum_acc<kTprB>(acc);
+                if (l == 0)
+                    for (int cc = 0; cc < n; ++cc) s_part[e0 + cc][r] = acc[cc];
+            }
+        }
+    }
+    __syncthreads();
+
+    // combine in pick order (tsx_moe_combine's arithmetic), into y
+    if (tid < T * kRowsB) {
+        const int t = tid / kRowsB, r = tid % kRowsB;
+        const float* wr = s_tab.wts + t * k;
+        const int32_t* ep = s_tab.ent_pos + t * k;
+        float acc = wr[0] * s_part[ep[0]][r];
+        for (int jj = 1; jj < k; ++jj) acc = __builtin_fmaf(wr[jj], s_part[ep[jj]][r], acc);
+        if (a.shared) {
+            const float gs = 1.0f / (1.0f + expf(-a.sgate[(int64_t) t * a.sg_stride]));
+            acc += gs * s_part[n_ent + t][r];
+        }
+        a.y[(int64_t) t * N + r0 + r] += acc;
+    }
+}
+
+template <typename F>
+int with_type(int type, F&& f) {
+    switch (type) {
+        case TSX_IQ3_XXS: return f(std::integral_constant<int, TSX_IQ3_XXS>{});
+        case TSX_IQ3_S: return f(std::integral_constant<int, TSX_IQ3_S>{});
+        case TSX_Q4_K: return f(std::integral_constant<int, TSX_Q4_K>{});
+        case TSX_Q8_0: return f(std::integral_constant<int, TSX_Q8_0>{});
+        default: return TSX_ERR_UNSUPPORTED;
+    }
+}
+
+// the largest rows_c in {32, 16, 8} whose gate + up chunk fits the slab and keeps 16-byte alignment
+int pick_rows_c(const tsx_expert_layout& L) {
+    for (int rc = kSliceA; rc >= 8; rc >>= 1)
+        if (2 * rc * L.gu_row <= (uint64_t) kSlabA && (rc * L.gu_row) % 16 == 0) return rc;
+    return 0;
+}
+size_t lds_a(const tsx_expert_layout& L, int n_tok) {
+    return (size_t) kSlabA + (size_t) n_tok * L.n_embd + (size_t) n_tok * (L.n_embd / 32) * 4;
+}
+size_t lds_b(const tsx_expert_layout& L, int n_tok, int k, bool shared) {
+    const size_t n16g = kRowsB * L.d_row / 16;
+    const int G = n_tok * k + (shared ? 1 : 0);
+    const size_t gc = std::max<size_t>(1, std::min<size_t>(G, (kSlabB / 16) / n16g));
+    const int P = n_tok * k + (shared ? n_tok : 0);
+    return gc * n16g * 16 + (size_t) P * L.n_ff + (size_t) P * (L.n_ff / 32) * 4;
+}
+size_t h_bytes(int n_tok, int k, int64_t n_ff) {  // codes then scales, the whole [n_tok * k + n_tok] positions
+    const size_t P = (size_t) (n_tok * k + n_tok);
+    return P * (size_t) n_ff + P * (size_t) (n_ff / 32) * 4;
+}
+constexpr size_t kMaxDynLds = 150 * 1024;
+// lets a kernel take more than 64 KB of dynamic LDS (gfx950 has 160 KB per workgroup); once per kernel
+bool set_max_lds(const void* kern) {
+    return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) kMaxDynLds) == hipSuccess;
+}
+
+}  // namespace
+}  // namespace tsx
+
+using namespace tsx;
+
+extern "C" {
+
+TSX_API size_t tsx_moe_decode_layer_scratch_bytes(int n_tok, int k, int64_t n_ff) {
+    if (n_tok < 1 || k < 1 || n_ff <= 0 || n_ff % 32 != 0) return 0;
+    return kTablesBytes + ((h_bytes(n_tok, k, n_ff) + 255) & ~(size_t) 255);
+}
+
+TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t stride, int n_expert, int k,
+                                 int n_tok, const float* logits, const float* x, const void* shared, const float* sgate,
+                                 int sg_stride, float* y, int32_t* ids, float* wts, void* scratch, void* stream) {
+    TSX_REQUIRE(Lp != nullptr, "tsx_moe_decode_layer: null layout");
+    const tsx_expert_layout L = *Lp;
+    if (!tsx_moe_expert_supported(L.gu_type, L.d_type, L.n_embd, L.n_ff) || L.n_embd > 4096 || L.n_ff > 1024 ||
+        L.n_ff % 128 != 0 || n_tok < 1 || n_tok > kMaxTok || k < 1 || n_tok * k > kMaxEnt || n_expert % 64 != 0 ||
+        n_expert > kMaxExperts || k > n_expert) {
+        set_error("tsx_moe_decode_layer: types (%d, %d) at %lld x %lld, %d tokens, %d experts top-%d not supported "
+                  "(n_embd <= 4096, n_ff a multiple of 128 up to 1024, 1..8 tokens, tokens * k <= 64, experts a "
+                  "multiple of 64 up to 512)",
+                  L.gu_type, L.d_type, (long long) L.n_embd, (long long) L.n_ff, n_tok, n_expert, k);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    const int rows_c = pick_rows_c(L);
+    if (rows_c == 0 || (kRowsB * L.d_row) % 16 != 0 || kRowsB * L.d_row > (uint64_t) kSlabB || L.up_off % 16 != 0 ||
+        L.down_off % 16 != 0 || lds_a(L, n_tok) > kMaxDynLds || lds_b(L, n_tok, k, shared != nullptr) > kMaxDynLds) {
+        set_error("tsx_moe_decode_layer: row sizes (%llu, %llu) do not tile into 16-byte LDS slabs",
+                  (unsigned long long) L.gu_row, (unsigned long long) L.d_row);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    TSX_REQUIRE(blobs && logits && x && y && ids && wts && scratch && (!shared || sgate),
+                "tsx_moe_decode_layer: a null pointer (sgate is needed with a shared expert)");
+    TSX_REQUIRE(aligned(blobs, 16) && stride % 16 == 0 && (!shared || aligned(shared, 16)) && aligned(scratch, 256) &&
+                    aligned(x, 16) && aligned(y, 4) && aligned(logits, 4),
+                "tsx_moe_decode_layer: blobs, stride, shared and x 16-byte aligned, scratch 256-byte aligned");
+    LayerArgs a;
+    a.L = L;
+    a.blobs = (const uint8_t*) blobs;
+    a.stride = stride;
+    a.n_expert = n_expert;
+    a.k = k;
+    a.n_tok = n_tok;
+    a.cap_groups = std::min(n_tok * k, n_expert);
+    a.logits = logits;
+    a.x = x;
+    a.shared = (const uint8_t*) shared;
+    a.sgate = sgate;
+    a.sg_stride = sg_stride;
+    a.rows_c = rows_c;
+    a.y = y;
+    a.ids = ids;
+    a.wts = wts;
+    a.tab = (LayerTables*) scratch;
+    const int P = n_tok * k + (shared ? n_tok : 0);  // h is packed for the positions this call uses
+    a.hc = (int8_t*) ((uint8_t*) scratch + kTablesBytes);
+    a.hd = (float*) (a.hc + (size_t) P * L.n_ff);
+    const hipStream_t s = (hipStream_t) stream;
+    int rc = with_type(L.gu_type, [&](auto T) {
+        auto kern = layer_gu_kernel<decltype(T)::value>;
+        static const bool once = set_max_lds((const void*) kern);
+        (void) once;
+        const dim3 grid((unsigned) (L.n_ff / kSliceA), (unsigned) (a.cap_groups + (shared ? 1 : 0)));
+        kern<<<grid, kThreadsA, lds_a(L, n_tok), s>>>(a);
+        return launch_status("tsx_moe_decode_layer/gate-up");
+    });
+    if (rc != TSX_OK) return rc;
+    return with_type(L.d_type, [&](auto T) {
+        auto kern = layer_down_kernel<decltype(T)::value>;
+        static const bool once = set_max_lds((const void*) kern);
+        (void) once;
+        kern<<<(unsigned) (L.n_embd / kRowsB), kThreadsB, lds_b(L, n_tok, k, shared != nullptr), s>>>(a);
+        return launch_status("tsx_moe_decode_layer/down");
+    });
+}
+
+}  // extern "C"

@@ -101,7 +101,7 @@ __global__ void __launch_bounds__(kThreads) mmq_rows_kernel(const uint8_t* __res
         float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
         for (int u = l; u < nu; u += LPR) {
             Unit wu;
-            unit_load<T>(wr, u, wu);
+            unit_load<T>(wr, u, wu, grid_const());
 #pragma unroll
             for (int c = 0; c < kNC; ++c) {
                 if (c < n) {

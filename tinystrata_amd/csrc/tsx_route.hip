@@ -12,23 +12,8 @@
 #include "tsx_common.hpp"
 #include "tsx_device.hpp"
 
-#include <cfloat>
-
 namespace tsx {
 namespace {
-
-constexpr int kMaxExperts = 512;
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 // one wave per token; expert e = lane + 64 i
 __global__ void __launch_bounds__(256) router_topk_kernel(const float* __restrict__ logits, int32_t* __restrict__ ids,
@@ -36,53 +21,7 @@ __global__ void __launch_bounds__(256) router_topk_kernel(const float* __restric
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= n_tok) return;
-    const int V = n_expert / 64;
-    const float* l = logits + (int64_t) t * n_expert;
-    float v[kMaxExperts / 64];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kMaxExperts / 64; ++i) {
-        v[i] = i < V ? l[lane + 64 * i] : -INFINITY;
-        mx = fmaxf(mx, v[i]);
-    }
-    mx = wave_max(mx);
-    float sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < kMaxExperts / 64; ++i) {
-        v[i] = i < V ? expf(v[i] - mx) : 0.f;
-        sum += v[i];
-    }
-    const float rcp = 1.0f / wave_sum(sum);
-#pragma unroll
-    for (int i = 0; i < kMaxExperts / 64; ++i) {
-        v[i] = i < V ? v[i] * rcp : -INFINITY;
-        if (__builtin_isnan(v[i])) v[i] = -FLT_MAX;
-    }
-    float selected = 0.f, selected_sum = 0.f;
-    for (int rank = 0; rank < k; ++rank) {
-        float best = v[0];
-        int expert = lane;
-#pragma unroll
-        for (int i = 1; i < kMaxExperts / 64; ++i)
-            if (v[i] > best) { best = v[i]; expert = lane + 64 * i; }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ob = __shfl_xor(best, o, 64);
-            const int oe = __shfl_xor(expert, o, 64);
-            if (ob > best || (ob == best && oe < expert)) { best = ob; expert = oe; }
-        }
-        if ((expert & 63) == lane) {
-#pragma unroll
-            for (int i = 0; i < kMaxExperts / 64; ++i)
-                if (i == expert / 64) v[i] = -INFINITY;
-            ids[(int64_t) t * k + rank] = expert;
-            selected_sum += best;
-        }
-        if (rank == lane) selected = best;
-    }
-    selected_sum = fmaxf(wave_sum(selected_sum), 6.103515625e-5f);
-    const float inv = 1.0f / selected_sum;
-    if (lane < k) wts[(int64_t) t * k + lane] = selected * inv;
+    route_token(logits + (int64_t) t * n_expert, n_expert, k, lane, ids + (int64_t) t * k, wts + (int64_t) t * k);
 }
 
 // decode grouping, one block: per-expert counts, then one thread lays out the groups and the entries in order

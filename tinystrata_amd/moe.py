@@ -78,7 +78,8 @@ def weights_from_pool(L: ExpertLayout, pool_dev: torch.Tensor, n_expert: int, or
 class MoELayer:
     """Runs one MoE layer for n_tok tokens with fixed buffers (decode path for n_tok <= decode_max)."""
 
-    def __init__(self, W: MoEWeights, k: int, n_tok: int, device: torch.device, decode_max: int = 8):
+    def __init__(self, W: MoEWeights, k: int, n_tok: int, device: torch.device, decode_max: int = 8,
+                 fused: bool = True):
         self.W, self.k, self.n_tok = W, k, n_tok
         L = W.L
         self.N, self.FF = int(L.n_embd), int(L.n_ff)
@@ -91,6 +92,11 @@ class MoELayer:
         self.wts = torch.empty((n_tok, k), dtype=f32, device=dev)
         self.parts = torch.empty((n_ent, self.N), dtype=f32, device=dev)
         self.sh = torch.empty((n_tok, self.N), dtype=f32, device=dev) if W.shared is not None else None
+        # the two-launch decode layer where its limits allow, else the reference's call sequence kernel by kernel
+        self.fused = fused and self.decode and n_ent <= 64 and self.N <= 4096 and self.FF <= 1024 and self.FF % 128 == 0
+        if self.fused:
+            self.lscratch = torch.empty(ops.decode_layer_scratch_bytes(n_tok, k, self.FF), dtype=torch.uint8,
+                                        device=dev)
         if self.decode:
             cap = min(n_ent, W.n_expert)
             self.cap_groups = cap
@@ -124,6 +130,10 @@ class MoELayer:
 
     def _decode(self, x, logits, sgate, y):
         W, L, k = self.W, self.W.L, self.k
+        if self.fused:
+            ops.moe_decode_layer(L, W.blobs, W.stride, W.n_expert, k, logits, x, y, self.ids, self.wts, self.lscratch,
+                                 shared=W.shared, sgate=sgate)
+            return
         ops.native_router_topk(logits, k, self.ids, self.wts)
         gp, gs, ng, ed, et = ops.group_entries(self.ids, k, W.n_expert, W.base, W.stride, bufs=self.grp)
         ops.quantize_q8_1_rows(x, self.xq)

@@ -94,6 +94,19 @@ def iq_mmvq(ggml_type: int, w, x_q8_1, n_in: int, n_out: int, ncols: int, y=None
 native_mmvq = iq_mmvq
 
 
+def decode_layer_scratch_bytes(n_tok: int, k: int, n_ff: int) -> int:
+    return lib().tsx_moe_decode_layer_scratch_bytes(n_tok, k, n_ff)
+
+
+def moe_decode_layer(L: ExpertLayout, blobs, stride: int, n_expert: int, k: int, logits, x, y, ids, wts, scratch,
+                     shared=None, sgate=None, sg_stride: int = 1, stream=None) -> None:
+    """y += the whole decode MoE layer of x (1..8 tokens) in two launches (tsx_moe_decode_layer)."""
+    n_tok = x.shape[0]
+    check(lib().tsx_moe_decode_layer(C.byref(L), _p(blobs), stride, n_expert, k, n_tok, _p(logits), _p(x), _p(shared),
+                                     _p(sgate), sg_stride, _p(y), _p(ids), _p(wts), _p(scratch), _stream(stream)),
+          "moe_decode_layer")
+
+
 # ------------------------------------------------------------------ routing
 def native_router_topk(logits: torch.Tensor, k: int, ids=None, weights=None, stream=None):
     n_tok, n_expert = logits.shape
