@@ -27,13 +27,14 @@ constexpr int kWave = 64;
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ codebooks and sign tables, built at compile time
-// A sign entry turns 8 signs into what negates the matching bytes of two grid words: w = (g ^ mask) + one, with
-// mask = 0xFF and one = 0x01 in every negated byte (no carry crosses a byte: every grid byte is > 0).
+// A sign entry turns 8 signs into what negates the matching bytes of two grid words: w = (g ^ mask) + (mask & 0x01..),
+// with mask = 0xFF in every negated byte (no carry crosses a byte: every grid byte is > 0).
 // xxs_sign is indexed by IQ3_XXS's 7-bit sign field (the 8th sign is the parity of the 7: ksigns_iq2xs),
-// s_sign by IQ3_S's sign byte.  Entry = {mask of values 0-3, mask of values 4-7, one 0-3, one 4-7}.
+// s_sign by IQ3_S's sign byte.  Entry = {mask of values 0-3, mask of values 4-7}.
 struct SignEntry {
-    uint32_t mask_lo, mask_hi, one_lo, one_hi;
+    uint32_t mask_lo, mask_hi;
 };
+__device__ __forceinline__ uint32_t apply_signs(uint32_t g, uint32_t mask) { return (g ^ mask) + (mask & 0x01010101u); }
 struct GridTables {
     uint32_t xxs[256];
     uint32_t s[512];
@@ -45,7 +46,7 @@ constexpr uint32_t spread_nibble(uint32_t nib) {  // bit i -> byte i = 1
 }
 constexpr SignEntry sign_entry(uint32_t s8) {
     const uint32_t lo = spread_nibble(s8 & 15u), hi = spread_nibble(s8 >> 4);
-    return SignEntry{lo * 0xFFu, hi * 0xFFu, lo, hi};
+    return SignEntry{lo * 0xFFu, hi * 0xFFu};
 }
 constexpr uint32_t parity7(uint32_t v) {
     uint32_t p = 0;
@@ -73,7 +74,7 @@ __device__ __forceinline__ GridRef grid_const() { return GridRef{kGrid.xxs, kGri
 // LDS words the tables of weight type T take (0 for types without a codebook)
 template <int T>
 constexpr int grid_lds_words() {
-    return T == TSX_IQ3_XXS ? 256 + 4 * 128 : T == TSX_IQ3_S ? 512 + 4 * 256 : 0;
+    return T == TSX_IQ3_XXS ? 256 + 2 * 128 : T == TSX_IQ3_S ? 512 + 2 * 256 : 0;
 }
 // the words of T's tables this thread copies (up to PER of them; word i = tid + n * k), loaded from the constant
 // tables: issue early, store later with grid_store
@@ -167,8 +168,8 @@ template <> __device__ __forceinline__ void unit_load<TSX_IQ3_XXS>(const uint8_t
         const SignEntry sg = g.xxs_sign[(aux >> (7 * l)) & 127u];
         const uint32_t q = l < 2 ? q0 : q1;
         const uint32_t i0 = (q >> (16 * (l & 1))) & 255u, i1 = (q >> (16 * (l & 1) + 8)) & 255u;
-        o.w[2 * l] = (int) ((g.xxs[i0] ^ sg.mask_lo) + sg.one_lo);
-        o.w[2 * l + 1] = (int) ((g.xxs[i1] ^ sg.mask_hi) + sg.one_hi);
+        o.w[2 * l] = (int) apply_signs(g.xxs[i0], sg.mask_lo);
+        o.w[2 * l + 1] = (int) apply_signs(g.xxs[i1], sg.mask_hi);
     }
     o.a = d * 0.25f * (float) (2 * (int) (aux >> 28) + 1);
     o.b = 0.f;
@@ -189,8 +190,8 @@ template <> __device__ __forceinline__ void unit_load<TSX_IQ3_S>(const uint8_t* 
         const int k0 = 2 * l, k1 = 2 * l + 1;
         const uint32_t i0 = ((q >> (8 * (k0 & 3))) & 255u) | (((qh >> k0) & 1u) << 8);
         const uint32_t i1 = ((q >> (8 * (k1 & 3))) & 255u) | (((qh >> k1) & 1u) << 8);
-        o.w[k0] = (int) ((g.s[i0] ^ sg.mask_lo) + sg.one_lo);
-        o.w[k1] = (int) ((g.s[i1] ^ sg.mask_hi) + sg.one_hi);
+        o.w[k0] = (int) apply_signs(g.s[i0], sg.mask_lo);
+        o.w[k1] = (int) apply_signs(g.s[i1], sg.mask_hi);
     }
     o.a = d * (float) (2 * (int) sc + 1);
     o.b = 0.f;
@@ -389,11 +390,38 @@ __device__ __forceinline__ void q8_1_store32(float x, tsx_block_q8_1* y, int i) 
 }
 
 
+// the wave's largest 32-bit unsigned value, the same in every lane (all 64 lanes active)
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    v = max(v, dpp_u32<0x140>(v));
+    const uint32_t a = (uint32_t) __builtin_amdgcn_readlane((int) v, 15), b = (uint32_t) __builtin_amdgcn_readlane((int) v, 31);
+    const uint32_t c = (uint32_t) __builtin_amdgcn_readlane((int) v, 47), d = (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
+    return max(max(a, b), max(c, d));
+}
+
+// the wave's smallest 32-bit unsigned value, the same in every lane (all 64 lanes active)
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0xB1>(v));
+    v = min(v, dpp_u32<0x4E>(v));
+    v = min(v, dpp_u32<0x141>(v));
+    v = min(v, dpp_u32<0x140>(v));
+    const uint32_t a = (uint32_t) __builtin_amdgcn_readlane((int) v, 15), b = (uint32_t) __builtin_amdgcn_readlane((int) v, 31);
+    const uint32_t c = (uint32_t) __builtin_amdgcn_readlane((int) v, 47), d = (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
+    return min(min(a, b), min(c, d));
+}
+
 // ------------------------------------------------------------------ routing of one token by one wave
 // Reference route_topk<NE,K> (src/kernels/cuda/native_router.cu:42-95): softmax with the max subtracted and one
 // reciprocal of the sum, NaN probabilities as -FLT_MAX, k rounds of argmax (ties to the lower id), weights divided by
 // max(sum of the picks, 6.1035e-5).  Expert e = lane + 64 i; n_expert a multiple of 64 up to kMaxExperts.  Each round
-// is one wave argmax on (probability, id) keys by DPP; the picked expert's key drops below every other.
+// takes the wave's largest probability key, then the lowest id holding it (two DPP reductions); the pick's key then
+// drops below every other.
 // ids / wts may point to global memory or LDS; every lane of the wave must call.
 constexpr int kMaxExperts = 512;
 __device__ __forceinline__ void route_token(const float* __restrict__ l, int n_expert, int k, int lane, int32_t* ids,
@@ -426,18 +454,21 @@ __device__ __forceinline__ void route_token(const float* __restrict__ l, int n_e
     float sel_sum = 0.f, my_p = 0.f;
     int my_id = 0;
     for (int r = 0; r < k; ++r) {
-        uint32_t hi = key[0], lo = ~(uint32_t) lane;
+        // each lane's best (key, lowest id among equal keys), the wave's largest key, then the lowest id holding it
+        uint32_t m = key[0];
+        int bi = 0;
 #pragma unroll
-        for (int i = 1; i < VM; ++i)
-            if (i < V) key_max(hi, lo, key[i], ~(uint32_t) (lane + 64 * i));
-        wave_key_max(hi, lo);
-        const int x = (int) ~lo;
-        const float p = key_value(hi);
-        if ((x & 63) == lane) {
-#pragma unroll
-            for (int i = 0; i < VM; ++i)
-                if (i == (x >> 6)) key[i] = 0u;
+        for (int i = 1; i < VM; ++i) {
+            const bool better = key[i] > m;
+            m = better ? key[i] : m;
+            bi = better ? i : bi;
         }
+        const uint32_t wm = wave_max_u32(m);
+        const int x = (int) wave_min_u32(m == wm ? (uint32_t) (lane + 64 * bi) : 0xFFFFFFFFu);
+#pragma unroll
+        for (int i = 0; i < VM; ++i)
+            if (i == (x >> 6) && lane == (x & 63)) key[i] = 0u;  // drops below every other key
+        const float p = key_value(wm);
         sel_sum += p;
         if (lane == r) {
             my_id = x;

@@ -46,16 +46,17 @@ constexpr int kMaxTok = 8;            // tokens per decode layer call
 constexpr int kMaxEnt = 64;           // routed entries (tokens x k)
 constexpr int kNC = 4;                // entries per pass over a row's units
 constexpr int kThreadsA = 1024;
+constexpr int kWavesA = kThreadsA / 64;
 constexpr int kSliceA = 32;           // gate (and up) rows per block of launch A: one Q8_1 block of h per entry
-constexpr int kSlabA = 64 * 1024;     // LDS bytes of a chunk of gate + up rows
-constexpr int kLoadsA = kSlabA / 16 / kThreadsA;
+constexpr int kSlabA = 64 * 1024;     // LDS bytes of a chunk of gate + up rows: 4 KB per wave
+constexpr int kWLoadsA = kSlabA / kWavesA / 16 / 64;  // 16-byte loads per lane of a wave's rows
 constexpr int kXLoads = 2;            // activation quads per thread per round of launch A
-constexpr int kThreadsB = 256;
+constexpr int kThreadsB = 512;
+constexpr int kWavesB = kThreadsB / 64;
 constexpr int kRowsB = 8;             // output rows per block of launch B
-constexpr int kSlabB = 48 * 1024;     // LDS bytes of down rows per group chunk
-constexpr int kLoadsB = kSlabB / 16 / kThreadsB;
-constexpr int kHLoads = 12;           // 16-byte pieces of h per thread per round of launch B
-constexpr int kTprB = 2;              // threads per (group, row) pair in launch B
+constexpr int kWLoadsB = 6;           // 16-byte loads per lane of a wave's rows (4 or 8 rows of one group)
+constexpr int kWaveSlabB = kWLoadsB * 64 * 16;
+constexpr int kHLoads = 6;            // 16-byte pieces of h per thread prefetched by launch B
 static_assert(kMaxTok <= kThreadsA / 64, "one wave per token in the routing");
 
 // the tables launch A leaves for launch B, at the start of the scratch buffer
@@ -68,7 +69,7 @@ struct LayerTables {
     float wts[kMaxEnt];
 };
 constexpr int kTableWords = sizeof(LayerTables) / 4;
-static_assert(kTableWords <= 2 * kThreadsB, "launch B reads the tables in two rounds");
+static_assert(kTableWords <= kThreadsB, "launch B reads the tables in one round");
 constexpr size_t kTablesBytes = (sizeof(LayerTables) + 255) & ~(size_t) 255;
 
 struct LayerArgs {
@@ -142,6 +143,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     __shared__ float s_wts[kMaxEnt];
     __shared__ int s_ngroups;
     __shared__ float s_gu[kMaxTok][2 * kSliceA];
+    __shared__ int s_xrow[kMaxTok];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int T = a.n_tok, k = a.k, n_ent = T * k;
@@ -215,30 +217,24 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     const int p0 = is_shared ? n_ent : s_grp_start[gy];
     const int n_e = is_shared ? T : s_grp_start[gy + 1] - p0;  // <= T: a token picks an expert once
 
-    // 2. the first chunk's rows in flight, then the activations
+    // 2. each wave's rows of the first chunk in flight, then the activations.  A chunk is 2 * rows_c rows (gate
+    //    rows, then up rows); wave w owns rpw of them and is the only reader of its LDS copy, so it starts computing
+    //    as soon as its own rows have arrived.
     const int rows_c = a.rows_c, nchunks = kSliceA / rows_c;
+    const int rpw = 2 * rows_c / kWavesA;          // rows per wave: 4, 2 or 1
+    const bool w_up = wave >= kWavesA / 2;
+    const int wr0 = rpw * (wave % (kWavesA / 2));  // the wave's first row within the chunk's gate (or up) rows
     const uint64_t gu_row = L.gu_row;
-    const int n16 = (int) (rows_c * gu_row / 16);  // 16-byte pieces of a chunk's gate (or up) rows
+    const int np = (int) (rpw * gu_row / 16);      // 16-byte pieces of the wave's rows (<= 64 * kWLoadsA)
     const int j = blockIdx.x;                      // slice: rows [32 j, 32 j + 32)
-    v4i reg[kLoadsA];
+    v4i reg[kWLoadsA];
     auto issue = [&](int c) {
-        const uint64_t off = (uint64_t) (kSliceA * j + c * rows_c) * gu_row;
-        const v4i* gsrc = (const v4i*) (blob + off);
-        const v4i* usrc = (const v4i*) (blob + L.up_off + off);
+        const v4i* src = (const v4i*) (blob + (w_up ? L.up_off : 0) + (uint64_t) (kSliceA * j + c * rows_c + wr0) * gu_row);
 #pragma unroll
-        for (int i = 0; i < kLoadsA; ++i) {  // unconditional (clamped) loads keep the wait counts exact
-            const int idx = min(tid + kThreadsA * i, 2 * n16 - 1);
-            reg[i] = __builtin_nontemporal_load(idx < n16 ? gsrc + idx : usrc + (idx - n16));
-        }
+        for (int i = 0; i < kWLoadsA; ++i)  // unconditional (clamped) loads keep the wait counts exact
+            reg[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, np - 1));
     };
-    v4i* slab = (v4i*) smem;
-    auto store = [&]() {
-#pragma unroll
-        for (int i = 0; i < kLoadsA; ++i) {
-            const int idx = tid + kThreadsA * i;
-            if (idx < 2 * n16) slab[idx] = reg[i];
-        }
-    };
+    v4i* wslab = (v4i*) smem + wave * (kSlabA / 16 / kWavesA);
     issue(0);
 
     // Q8_1 planes of the activations: every token's (row t) when they were prefetched, else the block's entries'
@@ -268,19 +264,22 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
             }
         }
     }
-    auto x_row = [&](int c) { return x_early ? (is_shared ? c : s_pos_ent[p0 + c] / k) : c; };
+    if (tid < n_e) s_xrow[tid] = x_early ? (is_shared ? tid : s_pos_ent[p0 + tid] / k) : tid;  // entry c's LDS row
     GridRef grid = grid_const();
     if constexpr (GW > 0) grid = grid_store<GT, GW>(s_grid, gw, tid, kThreadsA);
+    __syncthreads();  // activations and codebooks are in LDS
 
-    // 3. each chunk's rows against every entry: 2 * rows_c rows (gate, then up), tpr lanes per row
-    const int tpr = kThreadsA / (2 * rows_c);
-    const int rr = tid / tpr, l = tid % tpr;
+    // 3. each chunk: the wave's rows into its LDS slab, then against every entry, tpr lanes per row
+    const int tpr = 64 / rpw;
+    const int lr = lane / tpr, l = lane % tpr;
+    const uint8_t* row = (const uint8_t*) wslab + (uint64_t) lr * gu_row;
     for (int c = 0; c < nchunks; ++c) {
-        if (c > 0) __syncthreads();  // the previous chunk's rows are consumed
-        store();
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kWLoadsA; ++i)
+            if (lane + 64 * i < np) wslab[lane + 64 * i] = reg[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's LDS writes land before its reads
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         if (c + 1 < nchunks) issue(c + 1);
-        const uint8_t* row = (const uint8_t*) slab + (uint64_t) rr * gu_row;
         for (int e0 = 0; e0 < n_e; e0 += kNC) {
             const int n = min(kNC, n_e - e0);
             float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
@@ -291,7 +290,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
                 for (int cc = 0; cc < kNC; ++cc) {
                     if (cc < n) {
                         Act xa;
-                        const int xr = x_row(e0 + cc);
+                        const int xr = s_xrow[e0 + cc];
                         act_planes(s_xq + xr * N + 32 * u, s_xd + xr * NU + u, xa);
                         int S, M;
                         acc[cc] += unit_dot<GT>(w, xa, S, M);
@@ -304,10 +303,12 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
                 default: sum_acc<64>(acc); break;
             }
             if (l == 0) {
-                const int col = rr < rows_c ? c * rows_c + rr : kSliceA + c * rows_c + (rr - rows_c);
+                const int col = (w_up ? kSliceA : 0) + c * rows_c + wr0 + lr;
                 for (int cc = 0; cc < n; ++cc) s_gu[e0 + cc][col] = acc[cc];
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's reads are done before the next chunk
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
     __syncthreads();
 
@@ -333,6 +334,8 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     __shared__ __attribute__((aligned(16))) uint32_t s_grid[GW > 0 ? GW * kThreadsB : 4];
     __shared__ LayerTables s_tab;
     __shared__ float s_part[kMaxEnt + kMaxTok][kRowsB];
+    __shared__ const uint8_t* s_gsrc[kMaxEnt + 1];
+    __shared__ float s_sgate[kMaxTok];
 
     const int tid = threadIdx.x;
     const int T = a.n_tok, k = a.k, n_ent = T * k;
@@ -351,39 +354,42 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     v4i hv[kHLoads];
 #pragma unroll
     for (int i = 0; i < kHLoads; ++i) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
+    const float sg = a.shared ? a.sgate[(int64_t) min(tid, T - 1) * a.sg_stride] : 0.f;
+    const int ty = min(tid / kRowsB, T - 1), ry = tid % kRowsB;  // the y value this thread combines into
+    const float y0 = a.y[(int64_t) ty * N + r0 + ry];
     {
-        const uint32_t* src = (const uint32_t*) a.tab;
-        uint32_t* dst = (uint32_t*) &s_tab;
-        const uint32_t w0 = src[tid];
-        const uint32_t w1 = src[min(tid + kThreadsB, kTableWords - 1)];
-        if (tid < kTableWords) dst[tid] = w0;
-        if (tid + kThreadsB < kTableWords) dst[tid + kThreadsB] = w1;
+        const uint32_t w = ((const uint32_t*) a.tab)[min(tid, kTableWords - 1)];
+        if (tid < kTableWords) ((uint32_t*) &s_tab)[tid] = w;
+        if (tid < T) s_sgate[tid] = sg;
     }
     __syncthreads();
     const int ng = s_tab.n_groups;
     const int G = ng + (a.shared ? 1 : 0);  // group ng is the shared expert: positions [n_ent, n_ent + T)
-    auto grp_blob = [&](int g) { return g < ng ? a.blobs + (uint64_t) s_tab.grp_expert[g] * a.stride : a.shared; };
+    if (tid < G)  // where each group's 8 down rows start
+        s_gsrc[tid] = (tid < ng ? a.blobs + (uint64_t) s_tab.grp_expert[tid] * a.stride : a.shared) + L.down_off +
+                      (uint64_t) r0 * d_row;
+    __syncthreads();
     auto grp_lo = [&](int g) { return g < ng ? s_tab.grp_start[g] : n_ent; };
     auto grp_hi = [&](int g) { return g < ng ? s_tab.grp_start[g + 1] : n_ent + T; };
 
-    const int n16g = (int) (kRowsB * d_row / 16);  // 16-byte pieces of one group's 8 rows
-    const int gc = max(1, min(G, (kSlabB / 16) / n16g));
-    v4i reg[kLoadsB];
-    auto issue = [&](int g0) {
-        const int gn = min(gc, G - g0);
+    // work units: rb consecutive rows of one group (4, or 8 where 4 rows are not a whole number of 16-byte
+    // pieces); wave w takes units w, w + 8, ... and is the only reader of its LDS copy of them
+    const int rb = (4 * d_row) % 16 == 0 ? 4 : 8;
+    const int halves = kRowsB / rb, U = G * halves;
+    const int npu = (int) (rb * d_row / 16);  // 16-byte pieces of a unit (<= 64 * kWLoadsB)
+    const int wave = tid >> 6, lane = tid & 63;
+    v4i reg[kWLoadsB];
+    auto issue = [&](int un) {
+        const v4i* src = (const v4i*) (s_gsrc[un / halves] + (uint64_t) (un % halves) * rb * d_row);
 #pragma unroll
-        for (int i = 0; i < kLoadsB; ++i) {  // unconditional (clamped) loads keep the wait counts exact
-            const int idx = min(tid + kThreadsB * i, gn * n16g - 1);
-            const int g = g0 + idx / n16g;
-            const v4i* src = (const v4i*) (grp_blob(g) + L.down_off + (uint64_t) r0 * d_row);
-            reg[i] = __builtin_nontemporal_load(src + idx % n16g);
-        }
+        for (int i = 0; i < kWLoadsB; ++i)  // unconditional (clamped) loads keep the wait counts exact
+            reg[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, npu - 1));
     };
-    v4i* slab = (v4i*) smem;
-    issue(0);
+    v4i* wslab = (v4i*) (smem + (size_t) wave * kWaveSlabB);
+    if (wave < U) issue(wave);
 
     // h into LDS: the prefetched pieces, then any rest
-    int8_t* s_hq = (int8_t*) (smem + (size_t) gc * n16g * 16);
+    int8_t* s_hq = (int8_t*) (smem + (size_t) kWavesB * kWaveSlabB);
     float* s_hd = (float*) (s_hq + (size_t) P * FF);
     v4i* hdst = (v4i*) s_hq;
 #pragma unroll
@@ -392,43 +398,43 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     for (int idx = tid + kThreadsB * kHLoads; idx < nh; idx += kThreadsB) hdst[idx] = hsrc[idx];
     GridRef grid = grid_const();
     if constexpr (GW > 0) grid = grid_store<DT, GW>(s_grid, gw, tid, kThreadsB);
+    __syncthreads();  // h and codebooks are in LDS
 
-    const int l = tid % kTprB;
-    for (int g0 = 0; g0 < G; g0 += gc) {
-        const int gn = min(gc, G - g0);
-        if (g0 > 0) __syncthreads();  // the previous chunk's rows are consumed
+    const int tpr = 64 / rb;  // lanes per row: 16 or 8
+    const int lr = lane / tpr, l = lane % tpr;
+    const uint8_t* row = (const uint8_t*) wslab + (uint64_t) lr * d_row;
+    for (int un = wave; un < U; un += kWavesB) {
 #pragma unroll
-        for (int i = 0; i < kLoadsB; ++i) {
-            const int idx = tid + kThreadsB * i;
-            if (idx < gn * n16g) slab[idx] = reg[i];
-        }
-        __syncthreads();
-        if (g0 + gc < G) issue(g0 + gc);
-        for (int pair = tid / kTprB; pair < gn * kRowsB; pair += kThreadsB / kTprB) {
-            const int gl = pair / kRowsB, r = pair % kRowsB, g = g0 + gl;
-            const uint8_t* row = (const uint8_t*) slab + (uint64_t) pair * d_row;
-            const int q0 = grp_lo(g), q1 = grp_hi(g);
-            for (int e0 = q0; e0 < q1; e0 += kNC) {
-                const int n = min(kNC, q1 - e0);
-                float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
-                for (int u = l; u < NUd; u += kTprB) {
-                    Unit w;
-                    unit_load<DT>(row, u, w, grid);
+        for (int i = 0; i < kWLoadsB; ++i)
+            if (lane + 64 * i < npu) wslab[lane + 64 * i] = reg[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's LDS writes land before its reads
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (un + kWavesB < U) issue(un + kWavesB);
+        const int g = un / halves, r = (un % halves) * rb + lr;
+        const int q0 = grp_lo(g), q1 = grp_hi(g);
+        for (int e0 = q0; e0 < q1; e0 += kNC) {
+            const int n = min(kNC, q1 - e0);
+            float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
+            for (int u = l; u < NUd; u += tpr) {
+                Unit w;
+                unit_load<DT>(row, u, w, grid);
 #pragma unroll
-                    for (int cc = 0; cc < kNC; ++cc) {
-                        if (cc < n) {
-                            Act xa;
-                            act_planes(s_hq + (size_t) (e0 + cc) * FF + 32 * u, s_hd + (e0 + cc) * NUd + u, xa);
-                            int S, M;
-                            acc[cc] += unit_dot<DT>(w, xa, S, M);
-                        }
+                for (int cc = 0; cc < kNC; ++cc) {
+                    if (cc < n) {
+                        Act xa;
+                        act_planes(s_hq + (size_t) (e0 + cc) * FF + 32 * u, s_hd + (e0 + cc) * NUd + u, xa);
+                        int S, M;
+                        acc[cc] += unit_dot<DT>(w, xa, S, M);
                     }
                 }
-                sum_acc<kTprB>(acc);
-                if (l == 0)
-                    for (int cc = 0; cc < n; ++cc) s_part[e0 + cc][r] = acc[cc];
             }
+            if (tpr == 16) sum_acc<16>(acc);
+            else sum_acc<8>(acc);
+            if (l == 0)
+                for (int cc = 0; cc < n; ++cc) s_part[e0 + cc][r] = acc[cc];
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's reads are done before the next unit
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
     __syncthreads();
 
@@ -440,10 +446,10 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
         float acc = wr[0] * s_part[ep[0]][r];
         for (int jj = 1; jj < k; ++jj) acc = __builtin_fmaf(wr[jj], s_part[ep[jj]][r], acc);
         if (a.shared) {
-            const float gs = 1.0f / (1.0f + expf(-a.sgate[(int64_t) t * a.sg_stride]));
+            const float gs = 1.0f / (1.0f + expf(-s_sgate[t]));
             acc += gs * s_part[n_ent + t][r];
         }
-        a.y[(int64_t) t * N + r0 + r] += acc;
+        a.y[(int64_t) t * N + r0 + r] = y0 + acc;
     }
 }
 
@@ -458,32 +464,34 @@ int with_type(int type, F&& f) {
     }
 }
 
-// the largest rows_c in {32, 16, 8} whose gate + up chunk fits the slab and keeps 16-byte alignment
+// the largest rows_c in {32, 16, 8} whose gate + up chunk fits the slab with every wave's rows 16-byte aligned
 int pick_rows_c(const tsx_expert_layout& L) {
     for (int rc = kSliceA; rc >= 8; rc >>= 1)
-        if (2 * rc * L.gu_row <= (uint64_t) kSlabA && (rc * L.gu_row) % 16 == 0) return rc;
+        if (2 * rc * L.gu_row <= (uint64_t) kSlabA && ((2 * rc / kWavesA) * L.gu_row) % 16 == 0) return rc;
     return 0;
 }
 size_t lds_a(const tsx_expert_layout& L, int n_tok) {
     return (size_t) kSlabA + (size_t) n_tok * L.n_embd + (size_t) n_tok * (L.n_embd / 32) * 4;
 }
 size_t lds_b(const tsx_expert_layout& L, int n_tok, int k, bool shared) {
-    const size_t n16g = kRowsB * L.d_row / 16;
-    const int G = n_tok * k + (shared ? 1 : 0);
-    const size_t gc = std::max<size_t>(1, std::min<size_t>(G, (kSlabB / 16) / n16g));
     const int P = n_tok * k + (shared ? n_tok : 0);
-    return gc * n16g * 16 + (size_t) P * L.n_ff + (size_t) P * (L.n_ff / 32) * 4;
+    (void) L;
+    return (size_t) kWavesB * kWaveSlabB + (size_t) P * L.n_ff + (size_t) P * (L.n_ff / 32) * 4;
 }
 size_t h_bytes(int n_tok, int k, int64_t n_ff) {  // codes then scales, the whole [n_tok * k + n_tok] positions
     const size_t P = (size_t) (n_tok * k + n_tok);
     return P * (size_t) n_ff + P * (size_t) (n_ff / 32) * 4;
 }
-constexpr size_t kMaxDynLds = 150 * 1024;
-// lets a kernel take more than 64 KB of dynamic LDS (gfx950 has 160 KB per workgroup); once per kernel
-bool set_max_lds(const void* kern) {
-    return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) kMaxDynLds) == hipSuccess;
+constexpr size_t kLdsPerWorkgroup = 160 * 1024;  // gfx950
+constexpr size_t kMaxDynLds = 140 * 1024;        // the most any launch here asks for (the checks below hold it)
+// lets a kernel take more than the default 64 KB of dynamic LDS: up to what its static LDS leaves of the 160 KB.
+// Returns that limit (0 when the runtime refused); once per kernel.
+size_t set_max_lds(const void* kern) {
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, kern) != hipSuccess) return 0;
+    const size_t limit = kLdsPerWorkgroup - fa.sharedSizeBytes;
+    return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) limit) == hipSuccess ? limit : 0;
 }
-
 }  // namespace
 }  // namespace tsx
 
@@ -511,7 +519,8 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
         return TSX_ERR_UNSUPPORTED;
     }
     const int rows_c = pick_rows_c(L);
-    if (rows_c == 0 || (kRowsB * L.d_row) % 16 != 0 || kRowsB * L.d_row > (uint64_t) kSlabB || L.up_off % 16 != 0 ||
+    const uint64_t rb = (4 * L.d_row) % 16 == 0 ? 4 : 8;
+    if (rows_c == 0 || (rb * L.d_row) % 16 != 0 || rb * L.d_row > (uint64_t) kWaveSlabB || L.up_off % 16 != 0 ||
         L.down_off % 16 != 0 || lds_a(L, n_tok) > kMaxDynLds || lds_b(L, n_tok, k, shared != nullptr) > kMaxDynLds) {
         set_error("tsx_moe_decode_layer: row sizes (%llu, %llu) do not tile into 16-byte LDS slabs",
                   (unsigned long long) L.gu_row, (unsigned long long) L.d_row);
@@ -546,18 +555,26 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
     const hipStream_t s = (hipStream_t) stream;
     int rc = with_type(L.gu_type, [&](auto T) {
         auto kern = layer_gu_kernel<decltype(T)::value>;
-        static const bool once = set_max_lds((const void*) kern);
-        (void) once;
+        static const size_t limit = set_max_lds((const void*) kern);
+        const size_t lds = lds_a(L, n_tok);
+        if (lds > limit) {
+            set_error("tsx_moe_decode_layer: gate/up needs %zu B of LDS, %zu available", lds, limit);
+            return (int) TSX_ERR_UNSUPPORTED;
+        }
         const dim3 grid((unsigned) (L.n_ff / kSliceA), (unsigned) (a.cap_groups + (shared ? 1 : 0)));
-        kern<<<grid, kThreadsA, lds_a(L, n_tok), s>>>(a);
+        kern<<<grid, kThreadsA, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/gate-up");
     });
     if (rc != TSX_OK) return rc;
     return with_type(L.d_type, [&](auto T) {
         auto kern = layer_down_kernel<decltype(T)::value>;
-        static const bool once = set_max_lds((const void*) kern);
-        (void) once;
-        kern<<<(unsigned) (L.n_embd / kRowsB), kThreadsB, lds_b(L, n_tok, k, shared != nullptr), s>>>(a);
+        static const size_t limit = set_max_lds((const void*) kern);
+        const size_t lds = lds_b(L, n_tok, k, shared != nullptr);
+        if (lds > limit) {
+            set_error("tsx_moe_decode_layer: down needs %zu B of LDS, %zu available", lds, limit);
+            return (int) TSX_ERR_UNSUPPORTED;
+        }
+        kern<<<(unsigned) (L.n_embd / kRowsB), kThreadsB, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/down");
     });
 }
