@@ -1,13 +1,16 @@
-"""bench.py - TinyStrata's MoE expert matmul on one MI355X: the decode MoE layer stack.
+"""bench.py - TinyStrata's MoE expert matmul on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config decode|verify|plumb] [--eager] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config decode|verify|plumb|prefill|prefill_long] [--eager] [--no-cpu]
 
-A step is one token through 40 MoE layers with distinct weights (so the experts stream from HBM): per layer the
-router, the grouping, the Q8_1 activations, the grouped IQ3_XXS/IQ3_S experts, the shared expert and the weighted
-combine, each layer's output feeding the next (x <- x + moe(x)).  Inputs are synthetic (N(0,0.02) weights quantized
-by this library, N(0,1) activations and router logits) and resident in HBM before the timed region.
-Prints one JSON line (the driver's contract) with the roofline of the dominant launch and the reference CPU path
-timed on this host beside it.
+Default: the decode MoE layer stack of BASELINE.json configs[1].  A step is one pass of the hot path over one batch:
+  decode / verify / plumb   T tokens (1 or 4) through 40 MoE layers with distinct weights (so experts stream from
+                            HBM): routing, grouping, Q8_1 activations, the grouped experts (and the shared expert) and
+                            the weighted combine, each layer's output feeding the next (x <- x + moe(x)).
+  prefill / prefill_long    a prompt chunk (512 or 4096 tokens) through 4 such layers with the prompt path: routing,
+                            expert sort, gathered Q8_1 activations, int8-MFMA grouped gate/up, SwiGLU, down, combine.
+Inputs are synthetic (N(0,0.02) weights quantized by this library, N(0,1) activations, N(0,1) router logits with the
+config's skew) and resident in HBM before the timed region.  Prints one JSON line: the driver's contract plus the
+roofline of the dominant launch (timed with HIP events on its stream) and the reference CPU path timed on this host.
 """
 from __future__ import annotations
 
@@ -28,15 +31,34 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
 
 CONFIGS = {
-    # name: (gu, d, N, FF, E, k, shared, T, layers, description)
-    "decode": (18, 21, 2048, 512, 256, 8, True, 1, 40, "configs[1]: decode, 256 experts top-8 + shared, IQ3_XXS/IQ3_S"),
-    "verify": (18, 21, 2048, 512, 256, 8, True, 4, 40, "configs[2]: speculative verify M=4, correlated routing"),
-    "plumb": (8, 8, 2048, 768, 128, 8, False, 1, 40, "configs[0]: decode, 128 experts top-8, Q8_0"),
+    "decode": dict(gu=18, d=21, N=2048, FF=512, E=256, k=8, shared=True, T=1, layers=40, route="normal",
+                   desc="configs[1]: decode, 256 experts top-8 + shared, IQ3_XXS/IQ3_S"),
+    "verify": dict(gu=18, d=21, N=2048, FF=512, E=256, k=8, shared=True, T=4, layers=40, route="correlated",
+                   desc="configs[2]: speculative verify M=4, correlated routing"),
+    "plumb": dict(gu=8, d=8, N=2048, FF=768, E=128, k=8, shared=False, T=1, layers=40, route="normal",
+                  desc="configs[0]: decode, 128 experts top-8, Q8_0"),
+    "prefill": dict(gu=12, d=12, N=2048, FF=768, E=128, k=8, shared=False, T=512, layers=4, route="zipf1.1",
+                    desc="configs[3]: prefill 512 tokens, 128 experts top-8, Q4_K, Zipf(1.1) skew"),
+    "prefill_long": dict(gu=18, d=21, N=2048, FF=512, E=256, k=8, shared=True, T=4096, layers=4, route="zipf1.3",
+                         outliers=True, desc="configs[4]: prefill 4096 tokens, 256 experts top-8 + shared, IQ3, "
+                                              "Zipf(1.3) skew, 1% outlier channels x20"),
 }
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def make_logits(rng, cfg, layers):
+    T, E = cfg["T"], cfg["E"]
+    if cfg["route"] == "correlated":
+        z = rng.normal(0, 1, (layers, 1, E))
+        return (z + 0.5 * rng.normal(0, 1, (layers, T, E))).astype(np.float32)
+    if cfg["route"].startswith("zipf"):
+        s = float(cfg["route"][4:])
+        bias = np.stack([np.log(1.0 / (1 + rng.permutation(E)) ** s) for _ in range(layers)])[:, None, :]
+        return (rng.normal(0, 1, (layers, T, E)) + bias).astype(np.float32)
+    return rng.normal(0, 1, (layers, T, E)).astype(np.float32)
 
 
 def main() -> int:
@@ -50,7 +72,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs on one GPU; --gpus N > 1 is not supported (see DESIGN.md for the sharding plan)",
+        print("bench.py: this build runs on one GPU; --gpus N > 1 is not supported (the sharding plan is design only)",
               file=sys.stderr)
         return 2
 
@@ -58,7 +80,9 @@ def main() -> int:
 
     from tinystrata_amd import _lib, moe, ops
 
-    gu, d, N, FF, E, k, shared, T, layers, desc = CONFIGS[args.config]
+    cfg = CONFIGS[args.config]
+    gu, d, N, FF, E, k, shared, T, layers = (cfg[key] for key in ("gu", "d", "N", "FF", "E", "k", "shared", "T", "layers"))
+    prefill = T > 8
     dev = torch.device("cuda:0")
     _lib.check(_lib.lib().tsx_moe_init(0), "tsx_moe_init")
     L = ops.native_expert_layout(gu, d, N, FF)
@@ -83,11 +107,9 @@ def main() -> int:
 
     # ---------------------------------------------------------------- inputs
     x0 = rng.normal(0, 1, (T, N)).astype(np.float32)
-    if args.config == "verify":
-        z = rng.normal(0, 1, (layers, 1, E))
-        logits = (z + 0.5 * rng.normal(0, 1, (layers, T, E))).astype(np.float32)
-    else:
-        logits = rng.normal(0, 1, (layers, T, E)).astype(np.float32)
+    if cfg.get("outliers"):
+        x0[:, rng.choice(N, N // 100, replace=False)] *= 20.0
+    logits = make_logits(rng, cfg, layers)
     sg = rng.normal(0, 1, (layers, T)).astype(np.float32)
     x0_d = torch.from_numpy(x0).to(dev)
     x = torch.empty_like(x0_d)
@@ -128,28 +150,59 @@ def main() -> int:
     ms_step = start.elapsed_time(end) / args.steps
     value = layers * T / (ms_step / 1e3)
 
-    # distinct experts per layer (the bytes the layer must read)
+    # algorithmic work: each distinct expert's blob once per layer, the fp32 input and output rows; int8 ops
     ids_host = [ml.ids.cpu().numpy() for ml in mls]
     distinct_per_layer = [len(np.unique(i)) for i in ids_host]
     blob = L.bytes
     layer_bytes = [(n + int(shared)) * blob + 2 * T * N * 4 for n in distinct_per_layer]
     layer_ops = 2 * T * (k + int(shared)) * (3 * N * FF)
+    layer_s = ms_step / layers / 1e3
 
-    # ---------------------------------------------------------------- the dominant launch: the grouped experts
-    # back to back over the 40 layers' weights, HIP events on the stream they run on (torch's current stream)
-    reps = max(3, args.steps // 10)
+    # ---------------------------------------------------------------- the dominant launch, timed alone
+    reps = max(3, min(20, args.steps // 5))
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    if prefill:
+        # the grouped gate/up product (int8 MFMA) of every layer, on the current stream
+        def dom():
+            for ml in mls:
+                W = ml.W
+                ops.mmq_run(W.blobs, L.gu_type, 2 * FF, N, W.stride, W.n_expert, ml.mxq, ml.sort[0], None, ml.n_ent,
+                            ml.gu, 2 * FF)
+        gu_bytes = 2 * FF * L.gu_row
+        dom_bytes = float(np.mean([n * gu_bytes + ml.n_ent * (N + N // 32 * 8) + ml.n_ent * 2 * FF * 4
+                                   for n, ml in zip(distinct_per_layer, mls)]))
+        dom_ops = 2.0 * T * k * 2 * FF * N
+        kernel = "mmq_mfma_kernel (grouped gate/up product, v_mfma_i32_16x16x32_i8) per layer"
+    else:
+        # the whole expert work of a layer: tsx_moe_decode_layer's two launches, on the current stream
+        def dom():
+            for l, ml in enumerate(mls):
+                ops.moe_decode_layer(L, ml.W.blobs, ml.W.stride, ml.W.n_expert, k, logits_d[l], x, x, ml.ids, ml.wts,
+                                     ml.lscratch, shared=ml.W.shared, sgate=sg_d[l] if shared else None)
+        dom_bytes = float(np.mean(layer_bytes))
+        dom_ops = float(layer_ops)
+        kernel = "tsx_moe_decode_layer (layer_gu_kernel + layer_down_kernel) per layer"
+    dom()
     torch.cuda.synchronize()
     ev0.record()
     for _ in range(reps):
-        for ml in mls:
-            gp, gs, ng, ed, et = ml.grp
-            ops.native_expert_grouped(L, gp, gs, ng, ed, et, ml.cap_groups, ml.n_ent, ml.xq, ml.scratch, ml.parts)
+        dom()
     ev1.record()
     torch.cuda.synchronize()
-    dom_ms = ev0.elapsed_time(ev1) / (reps * layers)
-    dom_bytes = float(np.mean([n * blob + T * N // 32 * 36 + T * k * N * 4 for n in distinct_per_layer]))
-    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    dom_s = ev0.elapsed_time(ev1) / (reps * layers) / 1e3
+    achieved_gbs = dom_bytes / dom_s / 1e9
+    achieved_tops = dom_ops / dom_s / 1e12
+    if prefill and args.config == "prefill_long":
+        roof = {"bound": "mfma", "achieved": round(achieved_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s (int8)",
+                "frac": round(achieved_tops / INT8_PEAK_TOPS, 4)}
+    else:
+        roof = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved_gbs / HBM_PEAK_GBS, 4)}
+    roof.update({"traffic": None, "kernel": kernel, "launch_us": round(dom_s * 1e6, 3),
+                 "bytes_per_launch": int(dom_bytes), "int8_ops_per_launch": int(dom_ops),
+                 "hbm_frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+                 "int8_mfma_frac": round(achieved_tops / INT8_PEAK_TOPS, 4)})
 
     # ---------------------------------------------------------------- the reference CPU path on this host
     cpu = None
@@ -170,27 +223,19 @@ def main() -> int:
         "dtype": "int8",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.config}: {desc}",
+            "workload": f"{args.config}: {cfg['desc']}",
             "tokens": T, "layers": layers, "hidden": N, "expert_ff": FF, "experts": E, "top_k": k,
             "shared_expert": shared, "graph": graph is not None,
-            "layer_us": round(ms_step * 1e3 / layers, 3),
-            "layer_hbm_GBps": round(float(np.mean(layer_bytes)) / (ms_step / layers / 1e3) / 1e9, 1),
-            "layer_hbm_frac": round(float(np.mean(layer_bytes)) / (ms_step / layers / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "layer_us": round(layer_s * 1e6, 3),
+            "layer_hbm_GBps": round(float(np.mean(layer_bytes)) / layer_s / 1e9, 1),
+            "layer_hbm_frac": round(float(np.mean(layer_bytes)) / layer_s / 1e9 / HBM_PEAK_GBS, 4),
+            "layer_int8_TOPs": round(layer_ops / layer_s / 1e12, 3),
+            "layer_int8_mfma_frac": round(layer_ops / layer_s / 1e12 / INT8_PEAK_TOPS, 5),
             "layer_bytes": int(np.mean(layer_bytes)),
             "distinct_experts_per_layer": float(np.mean(distinct_per_layer)),
             "layer_int8_ops": layer_ops,
         },
-        "roofline": {
-            "kernel": "native_expert_grouped (gate/up, SwiGLU+Q8_1, down) per layer",
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "launch_us": round(dom_ms * 1e3, 3),
-            "bytes_per_launch": int(dom_bytes),
-        },
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
@@ -199,11 +244,14 @@ def main() -> int:
 
 def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared):
     """The reference CPU path (its own AVX-512/AVX2 expert rows, oracle/_ref) on this host's cores, over the same
-    routing and weights (each layer's used experts at distinct host addresses), timed for about cpu_seconds."""
+    routing and weights (each layer's used experts at distinct host addresses), timed for about cpu_seconds.  The
+    reference's pool takes at most 8 tokens per expert call, so a prompt chunk is sampled as its first 8 tokens."""
     import oracle as O
 
     threads = max(1, min(16, os.cpu_count() or 1))
     stride = pool.shape[1]
+    Tc = min(T, 8)
+    ids_host = [i[:Tc] for i in ids_host]
     # per layer: only the experts it uses, remapped to 0..u-1, plus its shared blob
     per = []
     for l in range(layers):
@@ -216,33 +264,34 @@ def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layer
     umax = max(b.shape[0] for b, _ in per)
     layer_stride = umax * stride
     host = np.zeros((layers, umax, stride), np.uint8)
-    ids = np.zeros((layers, T, k), np.int32)
+    ids = np.zeros((layers, Tc, k), np.int32)
     for l, (b, i) in enumerate(per):
         host[l, : b.shape[0]] = b
         ids[l] = i
-    wts = np.stack([ml.wts.cpu().numpy() for ml in mls]).astype(np.float32)
-    sgs = (1 / (1 + np.exp(-sg.astype(np.float64)))).astype(np.float32)
+    wts = np.stack([ml.wts.cpu().numpy()[:Tc] for ml in mls]).astype(np.float32)
+    sgs = (1 / (1 + np.exp(-sg[:, :Tc].astype(np.float64)))).astype(np.float32)
     if not O.ref_available():
-        return cpu_port(L, per, T, k, shared, args.cpu_seconds)
+        return cpu_port(L, per, Tc, k, shared, args.cpu_seconds)
     shared_ptr = None
     if shared:  # ref_moe_decode reads layer l's shared blob at shared + l * layer_stride: the last slot of every layer
         for l in range(layers):
             host[l, umax - 1] = per[l][0][-1]
         shared_ptr = host.ctypes.data + (umax - 1) * stride
-    x = x0.copy()
+    x = np.ascontiguousarray(x0[:Tc])
     R = O.ref()
-    one = R.ref_moe_decode(L.gu_type, L.d_type, L.n_embd, L.n_ff, T, k, layers, ids.ctypes.data, wts.ctypes.data,
+    one = R.ref_moe_decode(L.gu_type, L.d_type, L.n_embd, L.n_ff, Tc, k, layers, ids.ctypes.data, wts.ctypes.data,
                            host.ctypes.data, stride, layer_stride, shared_ptr, sgs.ctypes.data, x.ctypes.data,
                            threads, 2)
     iters = int(max(3, min(5000, args.cpu_seconds / max(one * layers, 1e-6))))
-    x = x0.copy()
-    per_layer = R.ref_moe_decode(L.gu_type, L.d_type, L.n_embd, L.n_ff, T, k, layers, ids.ctypes.data,
+    x = np.ascontiguousarray(x0[:Tc])
+    per_layer = R.ref_moe_decode(L.gu_type, L.d_type, L.n_embd, L.n_ff, Tc, k, layers, ids.ctypes.data,
                                  wts.ctypes.data, host.ctypes.data, stride, layer_stride, shared_ptr, sgs.ctypes.data,
                                  x.ctypes.data, threads, iters)
     isa = R.ref_isa()
-    return {"value": round(T / per_layer, 2), "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
+    return {"value": round(Tc / per_layer, 2), "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
             "sample": f"{iters} passes x {layers} layers, median pass; reference iq{isa}/kq256 rows, "
-                      f"Q8_K activations, {threads} pinned threads, {T} token(s)",
+                      f"Q8_K activations, {threads} pinned threads, {Tc} token(s)"
+                      + (f" (the first {Tc} of the {T}-token chunk)" if Tc < T else ""),
             "layer_us": round(per_layer * 1e6, 2)}
 
 

@@ -234,3 +234,36 @@ def test_expert_grouped_grid_groups_invariant():
         ops.native_expert_grouped(L, gp, gs, ng, ed, et, min(n_ent, E), n_ent, xq, scratch, out, grid_groups=gg)
         outs.append(host(out))
     assert (outs[0] == outs[1]).all() and (outs[0] == outs[2]).all()
+
+
+# ------------------------------------------------------------------ grouped prompt products
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("w_cols", [512, 2048])
+def test_mmq_run_skewed_groups(t, w_cols):
+    """One grouped product over experts with 0, 1, 17, 70 and 130 rows (tile tails, empty experts, several tiles),
+    rows scattered to dst through ids; against the oracle's per-row dot on the same Q8_1 codes.  Q8_0 at 2048 columns
+    takes the row-dot kernel (its 64-row slab does not fit LDS), every other case the int8-MFMA tiles."""
+    rng = np.random.default_rng(t + w_cols)
+    w_rows, counts = 128, [0, 70, 1, 130, 17]
+    n, total = len(counts), sum(counts)
+    bounds = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    W = [ops.quantize_weights(t, rng.normal(0, 0.02, (w_rows, w_cols)).astype(np.float32)) for _ in range(n)]
+    rb = W[0].shape[1]
+    eb = (w_rows * rb + 255) // 256 * 256
+    blob = np.zeros(n * eb, np.uint8)
+    for i, m in enumerate(W):
+        blob[i * eb: i * eb + m.size] = m.ravel()
+    x = rng.normal(0, 1, (total, w_cols)).astype(np.float32)
+    ids = rng.permutation(total).astype(np.int32)
+    xq = ops.mmq_quantize(dev(x), None, t, w_cols, w_cols, total)
+    dst = torch.full((total, w_rows), float("nan"), device="cuda")
+    ops.mmq_run(dev(blob), t, w_rows, w_cols, eb, n, xq, dev(bounds), dev(ids), total, dst, w_rows)
+    got = host(dst)
+    xb = O.quantize_q8_1(x)
+    exp = np.zeros((total, w_rows), np.float64)
+    for i in range(n):
+        r0, r1 = bounds[i], bounds[i + 1]
+        if r1 > r0:
+            exp[ids[r0:r1]] = O.mmvq_q8_1(t, W[i], w_cols, w_rows, xb[r0:r1], r1 - r0)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * np.abs(exp).max())

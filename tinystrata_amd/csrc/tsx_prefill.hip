@@ -127,6 +127,206 @@ __global__ void __launch_bounds__(kThreads) mmq_rows_kernel(const uint8_t* __res
     }
 }
 
+// ------------------------------------------------------------------ grouped product (int8 MFMA)
+// Block (weight-row tile bx, token tile by): 64 rows of one expert's matrix against 64 of the expert's sorted token
+// rows.  The token tiles of all experts are numbered in expert order (tiles of expert x = ceil(rows_x / 64)); each
+// block finds its expert from `bounds` with a block scan, so the launch needs no host-side count.  With
+// w_rows / 64 a multiple of 8 every token tile of one weight tile runs on the same XCD (blocks are dealt to the 8
+// XCDs round robin), so a weight tile is fetched from HBM once per XCD and then hits that XCD's L2.
+//
+// K advances one 256-value chunk at a time, software-pipelined: chunk c+1's weight blocks and activation codes are
+// loaded into registers while chunk c is multiplied.  A chunk's raw GGUF blocks (one per row) are copied into LDS
+// with 16-byte loads aligned down (IQ3 blocks are 98 / 110 bytes: a row's chunk starts at any even offset), decoded
+// to int8 (with the per-unit float scales, and for Q4_K the min terms) into a row-padded LDS tile next to the
+// chunk's activation codes, and each wave multiplies its 32 x 32 corner with v_mfma_i32_16x16x32_i8: one MFMA per
+// 32-value unit, so its int32 result is exactly the unit's integer sum S, scaled in fp32:
+// acc += a_w * d_x * S (- b_w * d_x * sum(q_x) for Q4_K).  The scaling costs ~3 VALU operations per output per unit
+// against 32 MACs on the matrix core, which is what bounds this kernel's MFMA utilisation.
+constexpr int kBM = 64, kBN = 64;
+constexpr int kChunk = 256;
+constexpr int kTileStride = kChunk + 16;  // LDS bytes per tile row: the padding spreads a wave's 8-byte reads over all banks
+constexpr int kMaxExpertsMmq = 512;
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+
+template <int T> constexpr int chunk_bytes() { return T == TSX_Q8_0 ? 8 * 34 : Fmt<T>::bytes; }
+// LDS bytes per row of a chunk's raw blocks: the block plus up to 15 bytes of alignment in front of it
+template <int T> constexpr int raw_stride() { return (chunk_bytes<T>() + 15 + 15) / 16 * 16; }
+template <int T> constexpr int raw_loads() { return (kBM * raw_stride<T>() / 16 + 255) / 256; }
+
+// exclusive prefix sum over the 256 threads of the block (v per thread), and the total
+__device__ __forceinline__ int block_scan_256(int v, int* s_wave, int& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += t;
+    }
+    if (lane == 63) s_wave[wave] = inc;
+    __syncthreads();
+    int off = 0;
+    for (int w = 0; w < wave; ++w) off += s_wave[w];
+    total = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+    return off + inc - v;
+}
+
+template <int T>
+__global__ void __launch_bounds__(256) mmq_mfma_kernel(const uint8_t* __restrict__ w, uint64_t expert_bytes,
+                                                       uint64_t row_bytes, int w_cols, int n_exp, MmqPlanes P,
+                                                       const int32_t* __restrict__ bounds, const int32_t* __restrict__ ids,
+                                                       float* __restrict__ dst, int64_t ld_dst) {
+    constexpr int GW = (grid_lds_words<T>() + 255) / 256;
+    constexpr int CB = chunk_bytes<T>(), RS = raw_stride<T>(), PR = RS / 16, RL = raw_loads<T>();
+    __shared__ __attribute__((aligned(16))) uint8_t s_raw[kBM * RS];
+    __shared__ __attribute__((aligned(16))) int8_t tA[kBM * kTileStride], tB[kBN * kTileStride];
+    __shared__ __attribute__((aligned(16))) uint32_t s_grid[GW > 0 ? GW * 256 : 4];
+    __shared__ __attribute__((aligned(16))) float s_aw[8][kBM], s_bw[8][kBM], s_dx[8][kBN], s_dm[8][kBN];
+    __shared__ int s_wave[4], s_x, s_tile0;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int bx = blockIdx.x, by = blockIdx.y;
+
+    // 1. which expert and which of its token tiles: two experts per thread, a block scan of tile counts
+    const int x0 = 2 * tid, x1 = 2 * tid + 1;
+    const int b0 = bounds[min(x0, n_exp)], b1 = bounds[min(x1, n_exp)], b2 = bounds[min(x1 + 1, n_exp)];
+    const int t0 = x0 < n_exp ? (b1 - b0 + kBN - 1) / kBN : 0, t1 = x1 < n_exp ? (b2 - b1 + kBN - 1) / kBN : 0;
+    int total;
+    const int start = block_scan_256(t0 + t1, s_wave, total);
+    if (by >= total) return;  // the whole block: fewer tiles than the grid's upper bound
+    if (start <= by && by < start + t0) { s_x = x0; s_tile0 = start; }
+    if (start + t0 <= by && by < start + t0 + t1) { s_x = x1; s_tile0 = start + t0; }
+    __syncthreads();
+    const int x = s_x;
+    const int row0 = bounds[x] + (by - s_tile0) * kBN;
+    const int nrows = min(kBN, bounds[x + 1] - row0);
+    const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) bx * kBM * row_bytes;
+    const int nu = w_cols / 32, nchunks = w_cols / kChunk;
+
+    // chunk c in flight: each row's raw block (the 16-byte pieces that hold it) and the activation codes / scales
+    v4i rw[RL], av[4];
+    float ad[2];
+    int am[2];
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < RL; ++i) {
+            const int q = min(tid + 256 * i, kBM * PR - 1), r = q / PR, pc = q - r * PR;
+            const uint64_t o = (uint64_t) r * row_bytes + (uint64_t) c * CB;
+            const int need = (int) (((o & 15) + CB + 15) / 16);  // pieces that start before the block's end
+            rw[i] = __builtin_nontemporal_load((const v4i*) (wbase + (o & ~(uint64_t) 15)) + min(pc, need - 1));
+        }
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int pi = tid + 256 * h, rr = pi >> 4, q = pi & 15;
+            av[h] = *(const v4i*) (P.q + (int64_t) (row0 + rr) * P.cols + kChunk * c + 16 * q);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int pi = tid + 256 * h, rr = pi >> 3, u = pi & 7;
+            const int64_t o = (int64_t) (row0 + rr) * nu + 8 * c + u;
+            ad[h] = P.d[o];
+            if constexpr (T == TSX_Q4_K) am[h] = P.m[o];
+        }
+    };
+    uint32_t gw[GW > 0 ? GW : 1];
+    if constexpr (GW > 0) grid_fetch<T, GW>(gw, tid, 256);
+    fetch(0);
+    GridRef grid = grid_const();
+    if constexpr (GW > 0) grid = grid_store<T, GW>(s_grid, gw, tid, 256);
+
+    const int wr = wave >> 1, wc = wave & 1;  // the wave's 32 x 32 corner
+    const int lr = lane & 15, lg = lane >> 4;
+    float acc[2][2][4];
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[ti][tj][i] = 0.f;
+
+    for (int c = 0; c < nchunks; ++c) {
+        // chunk c from registers into LDS
+#pragma unroll
+        for (int i = 0; i < RL; ++i)
+            if (tid + 256 * i < kBM * PR) ((v4i*) s_raw)[tid + 256 * i] = rw[i];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int pi = tid + 256 * h, rr = pi >> 4, q = pi & 15;
+            *(v4i*) (tB + rr * kTileStride + 16 * q) = av[h];
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int pi = tid + 256 * h, rr = pi >> 3, u = pi & 7;
+            s_dx[u][rr] = ad[h];
+            if constexpr (T == TSX_Q4_K) s_dm[u][rr] = ad[h] * (float) am[h];
+        }
+        __syncthreads();
+        if (c + 1 < nchunks) fetch(c + 1);
+        // decode: 64 rows x 8 units, two per thread
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int pr = tid + 256 * h, rr = pr >> 3, u = pr & 7;
+            const int off = (int) (((uint64_t) rr * row_bytes + (uint64_t) c * CB) & 15);
+            Unit wu;
+            unit_load<T>(s_raw + rr * RS + off, u, wu, grid);
+            v4i* dA = (v4i*) (tA + rr * kTileStride + 32 * u);
+            dA[0] = v4i{wu.w[0], wu.w[1], wu.w[2], wu.w[3]};
+            dA[1] = v4i{wu.w[4], wu.w[5], wu.w[6], wu.w[7]};
+            s_aw[u][rr] = wu.a;
+            if constexpr (T == TSX_Q4_K) s_bw[u][rr] = wu.b;
+        }
+        __syncthreads();
+        // the wave's corner, one MFMA per unit per 16 x 16 tile
+#pragma unroll 2
+        for (int u = 0; u < 8; ++u) {
+            long av8[2], bv8[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                av8[t] = *(const long*) (tA + (32 * wr + 16 * t + lr) * kTileStride + 32 * u + 8 * lg);
+                bv8[t] = *(const long*) (tB + (32 * wc + 16 * t + lr) * kTileStride + 32 * u + 8 * lg);
+            }
+            const float4 aw0 = *(const float4*) &s_aw[u][32 * wr + 4 * lg];
+            const float4 aw1 = *(const float4*) &s_aw[u][32 * wr + 16 + 4 * lg];
+            const float aws[2][4] = {{aw0.x, aw0.y, aw0.z, aw0.w}, {aw1.x, aw1.y, aw1.z, aw1.w}};
+#pragma unroll
+            for (int tj = 0; tj < 2; ++tj) {
+                const float dx = s_dx[u][32 * wc + 16 * tj + lr];
+#pragma unroll
+                for (int ti = 0; ti < 2; ++ti) {
+                    const v4i32 z = {0, 0, 0, 0};
+                    const v4i32 S = __builtin_amdgcn_mfma_i32_16x16x32_i8(av8[ti], bv8[tj], z, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[ti][tj][i] += (aws[ti][i] * dx) * (float) S[i];
+                }
+                if constexpr (T == TSX_Q4_K) {
+                    const float dm = s_dm[u][32 * wc + 16 * tj + lr];
+                    const float4 bw0 = *(const float4*) &s_bw[u][32 * wr + 4 * lg];
+                    const float4 bw1 = *(const float4*) &s_bw[u][32 * wr + 16 + 4 * lg];
+                    const float bws[2][4] = {{bw0.x, bw0.y, bw0.z, bw0.w}, {bw1.x, bw1.y, bw1.z, bw1.w}};
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[ti][tj][i] -= bws[ti][i] * dm;
+                }
+            }
+        }
+        __syncthreads();  // the tiles are consumed before the next chunk overwrites them
+    }
+
+    // out: row 4 lg + i of tile ti, token lr of tile tj
+#pragma unroll
+    for (int tj = 0; tj < 2; ++tj) {
+        const int tok = 32 * wc + 16 * tj + lr;
+        if (tok < nrows) {
+            const int64_t drow = ids ? ids[row0 + tok] : row0 + tok;
+#pragma unroll
+            for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    dst[drow * ld_dst + (int64_t) bx * kBM + 32 * wr + 16 * ti + 4 * lg + i] = acc[ti][tj][i];
+        }
+    }
+}
+
 __global__ void __launch_bounds__(kThreads) mmq_swiglu_kernel(const float* __restrict__ gu, float* __restrict__ h,
                                                               int64_t rows, int64_t n_ff, int interleaved) {
 #pragma clang fp contract(off)
@@ -205,11 +405,24 @@ TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
                 "tsx_moe_mmq_run: w, xq (256-byte aligned), bounds, dst, ld_dst >= w_rows, expert_bytes >= the matrix");
     if (p->n == 0 || p->w_rows == 0) return TSX_OK;
     const MmqPlanes P = planes((void*) p->xq, p->total_rows, p->w_cols);
+    const hipStream_t s = (hipStream_t) stream;
+    // the int8-MFMA tiles where the shape fits them, else the row-dot kernel
+    if (p->w_cols % kChunk == 0 && p->w_rows % kBM == 0 && p->n <= kMaxExpertsMmq && aligned(p->w, 16) &&
+        p->expert_bytes % 16 == 0) {
+        const int64_t max_tiles = (p->total_rows + kBN - 1) / kBN + p->n;
+        return with_type(p->type, [&](auto T) {
+            const dim3 grid((unsigned) (p->w_rows / kBM), (unsigned) max_tiles);
+            mmq_mfma_kernel<decltype(T)::value><<<grid, 256, 0, s>>>((const uint8_t*) p->w, p->expert_bytes, rb,
+                                                                     (int) p->w_cols, p->n, P, p->bounds, p->ids,
+                                                                     p->dst, p->ld_dst);
+            return launch_status("tsx_moe_mmq_run/mfma");
+        });
+    }
     const int lpr = lanes_per_row((int) (p->w_cols / 32)), rows = (kThreads / kWave) * (kWave / lpr);
     return with_type(p->type, [&](auto T) {
         return with_lpr(lpr, [&](auto LPR) {
             const dim3 grid((unsigned) ((p->w_rows + rows - 1) / rows), (unsigned) p->n);
-            mmq_rows_kernel<decltype(T)::value, decltype(LPR)::value><<<grid, kThreads, 0, (hipStream_t) stream>>>(
+            mmq_rows_kernel<decltype(T)::value, decltype(LPR)::value><<<grid, kThreads, 0, s>>>(
                 (const uint8_t*) p->w, p->expert_bytes, rb, (int) p->w_rows, (int) p->w_cols, P, p->bounds, p->ids, p->dst,
                 p->ld_dst);
             return launch_status("tsx_moe_mmq_run");
