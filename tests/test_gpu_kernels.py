@@ -239,12 +239,14 @@ def test_expert_grouped_grid_groups_invariant():
 # ------------------------------------------------------------------ grouped prompt products
 @pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("w_cols", [512, 2048])
-def test_mmq_run_skewed_groups(t, w_cols):
+@pytest.mark.parametrize("w_rows", [64, 128, 256, 96])
+def test_mmq_run_skewed_groups(t, w_cols, w_rows):
     """One grouped product over experts with 0, 1, 17, 70 and 130 rows (tile tails, empty experts, several tiles),
-    rows scattered to dst through ids; against the oracle's per-row dot on the same Q8_1 codes.  Q8_0 at 2048 columns
-    takes the row-dot kernel (its 64-row slab does not fit LDS), every other case the int8-MFMA tiles."""
-    rng = np.random.default_rng(t + w_cols)
-    w_rows, counts = 128, [0, 70, 1, 130, 17]
+    rows scattered to dst through ids; against the oracle's per-row dot on the same Q8_1 codes.  64, 128 and 256
+    weight rows take the MFMA tiles with 2, 4 and 8 waves (512 IQ3 columns: rows that start off 16-byte alignment),
+    96 rows the row-dot kernel."""
+    rng = np.random.default_rng(t + w_cols + w_rows)
+    counts = [0, 70, 1, 130, 17]
     n, total = len(counts), sum(counts)
     bounds = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     W = [ops.quantize_weights(t, rng.normal(0, 0.02, (w_rows, w_cols)).astype(np.float32)) for _ in range(n)]

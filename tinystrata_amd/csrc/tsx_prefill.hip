@@ -9,6 +9,8 @@
 //   d [rows_pad][cols/32] f32 the block scale, the fp16 value of the Q8_1 contract widened to float
 //   m [rows_pad][cols/32] i32 the sum of the block's codes (Q4_K's min term)
 // so a tile of tokens loads its codes with 16-byte loads and its scales without fp16 conversions.
+#include <type_traits>
+
 #include "tsx_common.hpp"
 #include "tsx_device.hpp"
 
@@ -127,34 +129,107 @@ __global__ void __launch_bounds__(kThreads) mmq_rows_kernel(const uint8_t* __res
     }
 }
 
-// ------------------------------------------------------------------ grouped product (int8 MFMA)
-// Block (weight-row tile bx, token tile by): 64 rows of one expert's matrix against 64 of the expert's sorted token
-// rows.  The token tiles of all experts are numbered in expert order (tiles of expert x = ceil(rows_x / 64)); each
-// block finds its expert from `bounds` with a block scan, so the launch needs no host-side count.  With
-// w_rows / 64 a multiple of 8 every token tile of one weight tile runs on the same XCD (blocks are dealt to the 8
-// XCDs round robin), so a weight tile is fetched from HBM once per XCD and then hits that XCD's L2.
+// ------------------------------------------------------------------ grouped product (f16 MFMA, exact unit sums)
+// Block (weight-row tile bx, token tile by): BM = 32 * NW rows of one expert's matrix against up to 64 of the
+// expert's sorted token rows.  The token tiles of all experts are numbered in expert order (tiles of expert x =
+// ceil(rows_x / 64)); each block finds its expert from `bounds` with a block scan, so the launch needs no host-side
+// count.
 //
-// K advances one 256-value chunk at a time, software-pipelined: chunk c+1's weight blocks and activation codes are
-// loaded into registers while chunk c is multiplied.  A chunk's raw GGUF blocks (one per row) are copied into LDS
-// with 16-byte loads aligned down (IQ3 blocks are 98 / 110 bytes: a row's chunk starts at any even offset), decoded
-// to int8 (with the per-unit float scales, and for Q4_K the min terms) into a row-padded LDS tile next to the
-// chunk's activation codes, and each wave multiplies its 32 x 32 corner with v_mfma_i32_16x16x32_i8: one MFMA per
-// 32-value unit, so its int32 result is exactly the unit's integer sum S, scaled in fp32:
-// acc += a_w * d_x * S (- b_w * d_x * sum(q_x) for Q4_K).  The scaling costs ~3 VALU operations per output per unit
-// against 32 MACs on the matrix core, which is what bounds this kernel's MFMA utilisation.
-constexpr int kBM = 64, kBN = 64;
+// The product runs on v_mfma_f32_16x16x32_f16, one MFMA per 32-value unit, with operands that are small integers and
+// therefore exact in fp16: A = the unit's weight codes times the integer part of its scale (IQ3_XXS: grid * sign *
+// (2 ls + 1) <= 1922; IQ3_S: <= 15 * 31; Q4_K: q * sc <= 945; Q8_0: the code), B = the Q8_1 activation codes.  Every
+// product and partial sum is an integer below 2^24, so the fp32 result is exactly (integer scale) x S, S the unit's
+// int8 dot product: the same integer sums as an int8 MFMA, with the integer scale already applied.  What is left per
+// output per unit is one fma with the activation scale, t += d_x * D; the weight row's float scale multiplies t once
+// per 256-value chunk (Q4_K adds its min term, one more fma; Q8_0 has a float scale per unit).  The int8 MFMA would
+// need three VALU operations per output per unit (convert, scale product, fma) against one here.
+//
+// Each wave owns 32 weight rows (two 16-row MFMA tiles) and every token of the tile, so it decodes its own A
+// fragments straight into registers from its raw GGUF blocks (staged per wave in LDS with 16-byte loads aligned
+// down) and only the activation tile is shared.  Activation codes are widened to fp16 while staging
+// (0x64XX - 1152 = XX - 128 per byte).  K advances one 256-value chunk at a time; the next chunk's weight pieces and
+// activation codes are in flight in registers while the current one is multiplied, and the activation tile is
+// double-buffered when LDS allows (one block barrier per chunk).
+constexpr int kBN = 64;
 constexpr int kChunk = 256;
-constexpr int kTileStride = kChunk + 16;  // LDS bytes per tile row: the padding spreads a wave's 8-byte reads over all banks
+constexpr int kBStride = kChunk + 8;  // fp16 per activation-tile row: 528 bytes puts 16 lanes' 16-byte reads on all banks
 constexpr int kMaxExpertsMmq = 512;
-typedef int v4i32 __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// fp16 codebooks: grid entry -> its 4 magnitudes as two fp16 pairs; 8 signs -> the XOR masks of four fp16 pairs
+struct HalfTables {
+    uint32_t xxs[2 * 256], xxs_sign[4 * 128], s[2 * 512], s_sign[4 * 256];
+};
+constexpr uint32_t half_bits(uint32_t v) {  // exact fp16 of an integer in [0, 2048)
+    if (v == 0) return 0;
+    int e = 0;
+    while ((v >> (e + 1)) != 0) ++e;
+    return (uint32_t) ((e + 15) << 10) | ((v << (10 - e)) & 1023u);
+}
+constexpr uint32_t half_pair(uint32_t a, uint32_t b) { return half_bits(a) | half_bits(b) << 16; }
+constexpr uint32_t sign_word(uint32_t s8, int k) { return ((s8 >> (2 * k)) & 1u) << 15 | ((s8 >> (2 * k + 1)) & 1u) << 31; }
+constexpr HalfTables make_half_tables() {
+    HalfTables h{};
+    for (int i = 0; i < 256; ++i) {
+        const uint32_t w = tsx_iq3xxs_word(i);
+        h.xxs[2 * i] = half_pair(w & 255u, (w >> 8) & 255u);
+        h.xxs[2 * i + 1] = half_pair((w >> 16) & 255u, w >> 24);
+    }
+    for (int i = 0; i < 512; ++i) {
+        const uint32_t w = tsx_iq3s_word(i);
+        h.s[2 * i] = half_pair(w & 255u, (w >> 8) & 255u);
+        h.s[2 * i + 1] = half_pair((w >> 16) & 255u, w >> 24);
+    }
+    for (uint32_t v = 0; v < 128; ++v)
+        for (int k = 0; k < 4; ++k) h.xxs_sign[4 * v + k] = sign_word(v | parity7(v) << 7, k);
+    for (uint32_t b = 0; b < 256; ++b)
+        for (int k = 0; k < 4; ++k) h.s_sign[4 * b + k] = sign_word(b, k);
+    return h;
+}
+static __constant__ const HalfTables kHalf = make_half_tables();
+template <int T> constexpr int half_grid_words() { return T == TSX_IQ3_XXS ? 512 : T == TSX_IQ3_S ? 1024 : 0; }
+template <int T> constexpr int half_table_words() { return 2 * half_grid_words<T>(); }
 
 template <int T> constexpr int chunk_bytes() { return T == TSX_Q8_0 ? 8 * 34 : Fmt<T>::bytes; }
-// LDS bytes per row of a chunk's raw blocks: the block plus up to 15 bytes of alignment in front of it
-template <int T> constexpr int raw_stride() { return (chunk_bytes<T>() + 15 + 15) / 16 * 16; }
-template <int T> constexpr int raw_loads() { return (kBM * raw_stride<T>() / 16 + 255) / 256; }
+// LDS bytes per row of a chunk's raw blocks: the block plus up to 15 bytes of alignment in front of it, rounded to
+// an odd number of 16-byte pieces so that 16 lanes reading the same field of 16 rows hit 16 different bank quads
+template <int T> constexpr int raw_stride() { return ((chunk_bytes<T>() + 15 + 15) / 16 | 1) * 16; }
+template <int T, int NW, int NB> constexpr int f16_lds_bytes() {
+    return NB * (kBN * kBStride * 2 + kBN * 8 * 4 * (T == TSX_Q4_K ? 2 : 1)) + NW * 32 * raw_stride<T>() +
+           half_table_words<T>() * 4 + NW * (32 * 4 + 8 * 32 * 4 * 3) + 64;
+}
+template <int T, int NW> constexpr int f16_buffers() { return f16_lds_bytes<T, NW, 2>() <= 150 * 1024 ? 2 : 1; }
 
-// exclusive prefix sum over the 256 threads of the block (v per thread), and the total
-__device__ __forceinline__ int block_scan_256(int v, int* s_wave, int& total) {
+__device__ __forceinline__ uint32_t hmul(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
+}
+__device__ __forceinline__ uint32_t hadd(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) + __builtin_bit_cast(h2, b));
+}
+__device__ __forceinline__ uint32_t hpair(uint32_t v) {  // small integer -> the fp16 pair (v, v)
+    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16) (float) v);
+    return h | h << 16;
+}
+// four signed bytes -> two fp16 pairs (bytes 0,1 and 2,3)
+__device__ __forceinline__ void i8_to_h(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    lo = hadd(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), 0xE480E480u);
+    hi = hadd(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), 0xE480E480u);
+}
+// four bytes in [0, 15] times the pair sc -> two fp16 pairs: (1024 + b) * sc - 1024 * sc, exact in one fma
+__device__ __forceinline__ void nib_to_h(uint32_t w, h2 sc, h2 nsc, uint32_t& lo, uint32_t& hi) {
+    const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u));
+    const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u));
+    lo = __builtin_bit_cast(uint32_t, a * sc + nsc);
+    hi = __builtin_bit_cast(uint32_t, b * sc + nsc);
+}
+__device__ __forceinline__ void wave_lds_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// exclusive prefix sum over the NT threads of the block (v per thread), and the total
+template <int NT>
+__device__ __forceinline__ int block_scan(int v, int* s_wave, int& total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int inc = v;
 #pragma unroll
@@ -165,166 +240,332 @@ __device__ __forceinline__ int block_scan_256(int v, int* s_wave, int& total) {
     if (lane == 63) s_wave[wave] = inc;
     __syncthreads();
     int off = 0;
-    for (int w = 0; w < wave; ++w) off += s_wave[w];
-    total = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+        off += w < wave ? s_wave[w] : 0;
+        total += s_wave[w];
+    }
     return off + inc - v;
 }
 
-template <int T>
-__global__ void __launch_bounds__(256) mmq_mfma_kernel(const uint8_t* __restrict__ w, uint64_t expert_bytes,
-                                                       uint64_t row_bytes, int w_cols, int n_exp, MmqPlanes P,
-                                                       const int32_t* __restrict__ bounds, const int32_t* __restrict__ ids,
-                                                       float* __restrict__ dst, int64_t ld_dst) {
-    constexpr int GW = (grid_lds_words<T>() + 255) / 256;
-    constexpr int CB = chunk_bytes<T>(), RS = raw_stride<T>(), PR = RS / 16, RL = raw_loads<T>();
-    __shared__ __attribute__((aligned(16))) uint8_t s_raw[kBM * RS];
-    __shared__ __attribute__((aligned(16))) int8_t tA[kBM * kTileStride], tB[kBN * kTileStride];
-    __shared__ __attribute__((aligned(16))) uint32_t s_grid[GW > 0 ? GW * 256 : 4];
-    __shared__ __attribute__((aligned(16))) float s_aw[8][kBM], s_bw[8][kBM], s_dx[8][kBN], s_dm[8][kBN];
-    __shared__ int s_wave[4], s_x, s_tile0;
+template <int T, int NW>
+__global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restrict__ w, uint64_t expert_bytes,
+                                                          uint64_t row_bytes, int w_cols, int n_exp, MmqPlanes P,
+                                                          const int32_t* __restrict__ bounds,
+                                                          const int32_t* __restrict__ ids, float* __restrict__ dst,
+                                                          int64_t ld_dst) {
+    constexpr int NT = 64 * NW, BM = 32 * NW, NB = f16_buffers<T, NW>();
+    constexpr int CB = chunk_bytes<T>(), RS = raw_stride<T>(), PR = RS / 16, RW = (32 * PR + 63) / 64;
+    constexpr int BP = kBN * 16 / NT, DP = kBN * 8 / NT, EPT = kMaxExpertsMmq / NT;
+    constexpr int TW = half_table_words<T>(), GW = half_grid_words<T>(), TPT = (TW + NT - 1) / NT;
+    constexpr bool Q4K = T == TSX_Q4_K, Q80 = T == TSX_Q8_0, IQ3S = T == TSX_IQ3_S;
+    __shared__ __attribute__((aligned(16))) _Float16 tB[NB][kBN * kBStride];
+    __shared__ __attribute__((aligned(16))) float s_dx[NB][kBN][8];
+    __shared__ __attribute__((aligned(16))) float s_dm[Q4K ? NB : 1][Q4K ? kBN : 1][8];
+    __shared__ __attribute__((aligned(16))) uint8_t s_raw[NW][32 * RS];
+    __shared__ __attribute__((aligned(16))) uint32_t s_tab[TW > 0 ? TW : 4];
+    __shared__ __attribute__((aligned(16))) float s_rd[NW][32];                          // row scale per chunk
+    __shared__ __attribute__((aligned(16))) uint32_t s_sc[IQ3S || Q4K ? NW : 1][8][32];  // integer scale as an fp16 pair
+    __shared__ __attribute__((aligned(16))) float s_uf[Q4K || Q80 ? NW : 1][8][32];      // Q4_K: dmin * m; Q8_0: d
+    __shared__ __attribute__((aligned(16))) uint2 s_am[T == TSX_IQ3_XXS ? NW : 1][8][32];  // IQ3_XXS: aux word, m pair
+    __shared__ int s_scan[NW], s_x, s_tile0;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int bx = blockIdx.x, by = blockIdx.y;
+    const int lr = lane & 15, g = lane >> 4;
 
-    // 1. which expert and which of its token tiles: two experts per thread, a block scan of tile counts
-    const int x0 = 2 * tid, x1 = 2 * tid + 1;
-    const int b0 = bounds[min(x0, n_exp)], b1 = bounds[min(x1, n_exp)], b2 = bounds[min(x1 + 1, n_exp)];
-    const int t0 = x0 < n_exp ? (b1 - b0 + kBN - 1) / kBN : 0, t1 = x1 < n_exp ? (b2 - b1 + kBN - 1) / kBN : 0;
+    // 1. which expert and which of its token tiles: EPT experts per thread, a block scan of tile counts
+    int tc[EPT], mine = 0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        const int x = EPT * tid + e;
+        const int b0 = bounds[min(x, n_exp)], b1 = bounds[min(x + 1, n_exp)];
+        tc[e] = x < n_exp ? (b1 - b0 + kBN - 1) / kBN : 0;
+        mine += tc[e];
+    }
     int total;
-    const int start = block_scan_256(t0 + t1, s_wave, total);
+    int start = block_scan<NT>(mine, s_scan, total);
     if (by >= total) return;  // the whole block: fewer tiles than the grid's upper bound
-    if (start <= by && by < start + t0) { s_x = x0; s_tile0 = start; }
-    if (start + t0 <= by && by < start + t0 + t1) { s_x = x1; s_tile0 = start + t0; }
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+        if (start <= by && by < start + tc[e]) {
+            s_x = EPT * tid + e;
+            s_tile0 = start;
+        }
+        start += tc[e];
+    }
     __syncthreads();
     const int x = s_x;
     const int row0 = bounds[x] + (by - s_tile0) * kBN;
     const int nrows = min(kBN, bounds[x + 1] - row0);
-    const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) bx * kBM * row_bytes;
+    const int ntt = (nrows + 15) >> 4;  // 16-token MFMA tiles with rows in them
+    const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) (bx * BM + 32 * wave) * row_bytes;
     const int nu = w_cols / 32, nchunks = w_cols / kChunk;
 
-    // chunk c in flight: each row's raw block (the 16-byte pieces that hold it) and the activation codes / scales
-    v4i rw[RL], av[4];
-    float ad[2];
-    int am[2];
+    // chunk c in flight: this wave's raw weight pieces, the block's share of activation codes and scales
+    v4i rw[RW], av[BP];
+    float ad[DP];
+    int am[DP];
     auto fetch = [&](int c) {
 #pragma unroll
-        for (int i = 0; i < RL; ++i) {
-            const int q = min(tid + 256 * i, kBM * PR - 1), r = q / PR, pc = q - r * PR;
+        for (int i = 0; i < RW; ++i) {
+            const int q = min(lane + 64 * i, 32 * PR - 1), r = q / PR, pc = q - r * PR;
             const uint64_t o = (uint64_t) r * row_bytes + (uint64_t) c * CB;
             const int need = (int) (((o & 15) + CB + 15) / 16);  // pieces that start before the block's end
             rw[i] = __builtin_nontemporal_load((const v4i*) (wbase + (o & ~(uint64_t) 15)) + min(pc, need - 1));
         }
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const int pi = tid + 256 * h, rr = pi >> 4, q = pi & 15;
+        for (int h = 0; h < BP; ++h) {
+            const int pi = tid + NT * h, rr = pi >> 4, q = pi & 15;
             av[h] = *(const v4i*) (P.q + (int64_t) (row0 + rr) * P.cols + kChunk * c + 16 * q);
         }
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int pi = tid + 256 * h, rr = pi >> 3, u = pi & 7;
+        for (int h = 0; h < DP; ++h) {
+            const int e = tid + NT * h, rr = e >> 3, u = e & 7;
             const int64_t o = (int64_t) (row0 + rr) * nu + 8 * c + u;
             ad[h] = P.d[o];
-            if constexpr (T == TSX_Q4_K) am[h] = P.m[o];
+            if constexpr (Q4K) am[h] = P.m[o];
         }
     };
-    uint32_t gw[GW > 0 ? GW : 1];
-    if constexpr (GW > 0) grid_fetch<T, GW>(gw, tid, 256);
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < RW; ++i)
+            if (lane + 64 * i < 32 * PR) ((v4i*) s_raw[wave])[lane + 64 * i] = rw[i];
+#pragma unroll
+        for (int h = 0; h < BP; ++h) {
+            const int pi = tid + NT * h, rr = pi >> 4, q = pi & 15;
+            uint32_t o[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) i8_to_h((uint32_t) av[h][k], o[2 * k], o[2 * k + 1]);
+            v4i* d = (v4i*) (&tB[buf][rr * kBStride + 16 * q]);
+            d[0] = v4i{(int) o[0], (int) o[1], (int) o[2], (int) o[3]};
+            d[1] = v4i{(int) o[4], (int) o[5], (int) o[6], (int) o[7]};
+        }
+#pragma unroll
+        for (int h = 0; h < DP; ++h) {
+            const int e = tid + NT * h, rr = e >> 3, u = e & 7;
+            s_dx[buf][rr][u] = ad[h];
+            if constexpr (Q4K) s_dm[buf][rr][u] = ad[h] * (float) am[h];
+        }
+    };
+
+    uint32_t tw[TPT > 0 ? TPT : 1];
+    if constexpr (TW > 0) {
+        const uint32_t* src = T == TSX_IQ3_XXS ? kHalf.xxs : kHalf.s;
+        const uint32_t* sgn = T == TSX_IQ3_XXS ? kHalf.xxs_sign : kHalf.s_sign;
+#pragma unroll
+        for (int k = 0; k < TPT; ++k) {
+            const int i = min(tid + NT * k, TW - 1);
+            tw[k] = i < GW ? src[i] : sgn[i - GW];
+        }
+    }
     fetch(0);
-    GridRef grid = grid_const();
-    if constexpr (GW > 0) grid = grid_store<T, GW>(s_grid, gw, tid, 256);
+    if constexpr (TW > 0) {
+#pragma unroll
+        for (int k = 0; k < TPT; ++k)
+            if (tid + NT * k < TW) s_tab[tid + NT * k] = tw[k];
+    }
+    stage(0);
+    if (nchunks > 1) fetch(1);
+    __syncthreads();
 
-    const int wr = wave >> 1, wc = wave & 1;  // the wave's 32 x 32 corner
-    const int lr = lane & 15, lg = lane >> 4;
-    float acc[2][2][4];
+    // the chunk loop, specialised on the number of 16-token tiles that hold rows (no per-tile branches inside)
+    auto run = [&](auto ntt_c) {
+        constexpr int NTT = decltype(ntt_c)::value;
+        float acc[2][NTT][4], tacc[2][NTT][4];
 #pragma unroll
-    for (int ti = 0; ti < 2; ++ti)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int tj = 0; tj < 2; ++tj)
+            for (int tj = 0; tj < NTT; ++tj)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[ti][tj][i] = 0.f;
+                for (int i = 0; i < 4; ++i) acc[t][tj][i] = tacc[t][tj][i] = 0.f;
 
-    for (int c = 0; c < nchunks; ++c) {
-        // chunk c from registers into LDS
+        for (int c = 0; c < nchunks; ++c) {
+            const int buf = NB == 2 ? (c & 1) : 0;
+            const _Float16* B = tB[buf];
+            const uint8_t* slab = s_raw[wave];
+            // the wave's rows: per-row and per-unit factors (lane = row r, units 4 hl .. 4 hl + 3)
+            {
+                const int r = lane & 31, hl = lane >> 5;
+                const uint8_t* b = slab + r * RS + (int) (((uint64_t) r * row_bytes + (uint64_t) c * CB) & 15);
+                if constexpr (T == TSX_IQ3_XXS) {
+                    if (hl == 0) s_rd[wave][r] = 0.25f * h2f((uint16_t) ld16(b));
 #pragma unroll
-        for (int i = 0; i < RL; ++i)
-            if (tid + 256 * i < kBM * PR) ((v4i*) s_raw)[tid + 256 * i] = rw[i];
+                    for (int k = 0; k < 4; ++k) {
+                        const int j = 4 * hl + k;
+                        const uint32_t aux = ld32a2(b + 66 + 4 * j);
+                        s_am[wave][j][r] = uint2{aux, hpair(2 * (aux >> 28) + 1)};
+                    }
+                } else if constexpr (IQ3S) {
+                    if (hl == 0) s_rd[wave][r] = h2f((uint16_t) ld16(b));
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            const int pi = tid + 256 * h, rr = pi >> 4, q = pi & 15;
-            *(v4i*) (tB + rr * kTileStride + 16 * q) = av[h];
-        }
+                    for (int k = 0; k < 4; ++k) {
+                        const int j = 4 * hl + k;
+                        s_sc[wave][j][r] = hpair(2 * ((b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u) + 1);
+                    }
+                } else if constexpr (Q4K) {
+                    const float d = h2f((uint16_t) ld16(b)), dmin = h2f((uint16_t) ld16(b + 2));
+                    if (hl == 0) s_rd[wave][r] = d;
+                    const uint8_t* s12 = b + 4;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int pi = tid + 256 * h, rr = pi >> 3, u = pi & 7;
-            s_dx[u][rr] = ad[h];
-            if constexpr (T == TSX_Q4_K) s_dm[u][rr] = ad[h] * (float) am[h];
-        }
-        __syncthreads();
-        if (c + 1 < nchunks) fetch(c + 1);
-        // decode: 64 rows x 8 units, two per thread
+                    for (int k = 0; k < 4; ++k) {
+                        const int j = 4 * hl + k;
+                        int sc, m;
+                        if (j < 4) {
+                            sc = s12[j] & 63;
+                            m = s12[j + 4] & 63;
+                        } else {
+                            sc = (s12[j + 4] & 15) | ((s12[j - 4] >> 6) << 4);
+                            m = (s12[j + 4] >> 4) | ((s12[j] >> 6) << 4);
+                        }
+                        s_sc[wave][j][r] = hpair((uint32_t) sc);
+                        s_uf[wave][j][r] = dmin * (float) m;
+                    }
+                } else {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int pr = tid + 256 * h, rr = pr >> 3, u = pr & 7;
-            const int off = (int) (((uint64_t) rr * row_bytes + (uint64_t) c * CB) & 15);
-            Unit wu;
-            unit_load<T>(s_raw + rr * RS + off, u, wu, grid);
-            v4i* dA = (v4i*) (tA + rr * kTileStride + 32 * u);
-            dA[0] = v4i{wu.w[0], wu.w[1], wu.w[2], wu.w[3]};
-            dA[1] = v4i{wu.w[4], wu.w[5], wu.w[6], wu.w[7]};
-            s_aw[u][rr] = wu.a;
-            if constexpr (T == TSX_Q4_K) s_bw[u][rr] = wu.b;
-        }
-        __syncthreads();
-        // the wave's corner, one MFMA per unit per 16 x 16 tile
-#pragma unroll 2
-        for (int u = 0; u < 8; ++u) {
-            long av8[2], bv8[2];
+                    for (int k = 0; k < 4; ++k) {
+                        const int j = 4 * hl + k;
+                        s_uf[wave][j][r] = h2f((uint16_t) ld16(b + 34 * j));
+                    }
+                }
+            }
+            wave_lds_order();
+            // the lane's decode rows (one per 16-row tile)
+            const uint8_t* blk[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                av8[t] = *(const long*) (tA + (32 * wr + 16 * t + lr) * kTileStride + 32 * u + 8 * lg);
-                bv8[t] = *(const long*) (tB + (32 * wc + 16 * t + lr) * kTileStride + 32 * u + 8 * lg);
+                const int r = 16 * t + lr;
+                blk[t] = slab + r * RS + (int) (((uint64_t) r * row_bytes + (uint64_t) c * CB) & 15);
             }
-            const float4 aw0 = *(const float4*) &s_aw[u][32 * wr + 4 * lg];
-            const float4 aw1 = *(const float4*) &s_aw[u][32 * wr + 16 + 4 * lg];
-            const float aws[2][4] = {{aw0.x, aw0.y, aw0.z, aw0.w}, {aw1.x, aw1.y, aw1.z, aw1.w}};
+#pragma unroll 1
+            for (int up = 0; up < 8; up += 2) {
+              float2 dx2[NTT], dm2[NTT];
 #pragma unroll
-            for (int tj = 0; tj < 2; ++tj) {
-                const float dx = s_dx[u][32 * wc + 16 * tj + lr];
+              for (int tj = 0; tj < NTT; ++tj) {
+                  dx2[tj] = *(const float2*) &s_dx[buf][16 * tj + lr][up];
+                  if constexpr (Q4K) dm2[tj] = *(const float2*) &s_dm[buf][16 * tj + lr][up];
+              }
 #pragma unroll
-                for (int ti = 0; ti < 2; ++ti) {
-                    const v4i32 z = {0, 0, 0, 0};
-                    const v4i32 S = __builtin_amdgcn_mfma_i32_16x16x32_i8(av8[ti], bv8[tj], z, 0, 0, 0);
+              for (int k = 0; k < 2; ++k) {
+                const int u = up + k;
+                v4i A[2];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[ti][tj][i] += (aws[ti][i] * dx) * (float) S[i];
+                for (int t = 0; t < 2; ++t) {
+                    const uint8_t* b = blk[t];
+                    const int r = 16 * t + lr;
+                    uint32_t f[4];
+                    if constexpr (T == TSX_IQ3_XXS) {
+                        const uint32_t qp = ld16(b + 2 + 8 * u + 2 * g);
+                        const uint2 am = s_am[wave][u][r];
+                        const uint32_t aux = am.x, m = am.y;
+                        const uint2 g0 = *(const uint2*) (s_tab + 2 * (qp & 255u));
+                        const uint2 g1 = *(const uint2*) (s_tab + 2 * (qp >> 8));
+                        const uint4 sm = *(const uint4*) (s_tab + GW + 4 * ((aux >> (7 * g)) & 127u));
+                        f[0] = hmul(g0.x ^ sm.x, m);
+                        f[1] = hmul(g0.y ^ sm.y, m);
+                        f[2] = hmul(g1.x ^ sm.z, m);
+                        f[3] = hmul(g1.y ^ sm.w, m);
+                    } else if constexpr (IQ3S) {
+                        const uint32_t qp = ld16(b + 2 + 8 * u + 2 * g);
+                        const uint32_t qh = (uint32_t) b[66 + u] >> (2 * g);
+                        const uint32_t i0 = (qp & 255u) | (qh & 1u) << 8, i1 = (qp >> 8) | (qh & 2u) << 7;
+                        const uint2 g0 = *(const uint2*) (s_tab + 2 * i0);
+                        const uint2 g1 = *(const uint2*) (s_tab + 2 * i1);
+                        const uint4 sm = *(const uint4*) (s_tab + GW + 4 * (uint32_t) b[74 + 4 * u + g]);
+                        const uint32_t m = s_sc[wave][u][r];
+                        f[0] = hmul(g0.x ^ sm.x, m);
+                        f[1] = hmul(g0.y ^ sm.y, m);
+                        f[2] = hmul(g1.x ^ sm.z, m);
+                        f[3] = hmul(g1.y ^ sm.w, m);
+                    } else if constexpr (Q4K) {
+                        const uint8_t* q = b + 16 + 32 * (u >> 1) + 8 * g;
+                        const int sh = 4 * (u & 1);
+                        const uint32_t w0 = (ld32a2(q) >> sh) & 0x0F0F0F0Fu, w1 = (ld32a2(q + 4) >> sh) & 0x0F0F0F0Fu;
+                        const h2 sc = __builtin_bit_cast(h2, s_sc[wave][u][r]);
+                        const h2 nsc = sc * (_Float16) -1024.0f;
+                        nib_to_h(w0, sc, nsc, f[0], f[1]);
+                        nib_to_h(w1, sc, nsc, f[2], f[3]);
+                    } else {
+                        const uint8_t* q = b + 34 * u + 2 + 8 * g;
+                        i8_to_h(ld32a2(q), f[0], f[1]);
+                        i8_to_h(ld32a2(q + 4), f[2], f[3]);
+                    }
+                    A[t] = v4i{(int) f[0], (int) f[1], (int) f[2], (int) f[3]};
                 }
-                if constexpr (T == TSX_Q4_K) {
-                    const float dm = s_dm[u][32 * wc + 16 * tj + lr];
-                    const float4 bw0 = *(const float4*) &s_bw[u][32 * wr + 4 * lg];
-                    const float4 bw1 = *(const float4*) &s_bw[u][32 * wr + 16 + 4 * lg];
-                    const float bws[2][4] = {{bw0.x, bw0.y, bw0.z, bw0.w}, {bw1.x, bw1.y, bw1.z, bw1.w}};
+                // per-output-row unit factors (Q4_K min, Q8_0 scale): rows 16 t + 4 g + i
+                float4 uf[2];
+                if constexpr (Q4K || Q80) {
 #pragma unroll
-                    for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[ti][tj][i] -= bws[ti][i] * dm;
+                    for (int t = 0; t < 2; ++t) uf[t] = *(const float4*) &s_uf[wave][u][16 * t + 4 * g];
                 }
+#pragma unroll
+                for (int tj = 0; tj < NTT; ++tj) {
+                    const int tok = 16 * tj + lr;
+                    const v4i Bf = *(const v4i*) (B + tok * kBStride + 32 * u + 8 * g);
+                    const float dx = k == 0 ? dx2[tj].x : dx2[tj].y;
+                    float dm = 0.f;
+                    if constexpr (Q4K) dm = k == 0 ? dm2[tj].x : dm2[tj].y;
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const v4f z = {0.f, 0.f, 0.f, 0.f};
+                        const v4f D = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, A[t]),
+                                                                             __builtin_bit_cast(v8h, Bf), z, 0, 0, 0);
+                        const float ufa[4] = {uf[t].x, uf[t].y, uf[t].z, uf[t].w};
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            if constexpr (Q80) {
+                                acc[t][tj][i] += (ufa[i] * dx) * D[i];
+                            } else {
+                                tacc[t][tj][i] += dx * D[i];
+                                if constexpr (Q4K) acc[t][tj][i] -= ufa[i] * dm;
+                            }
+                        }
+                    }
+                }
+              }
+            }
+            if constexpr (!Q80) {  // the chunk's row scale
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const float4 rd4 = *(const float4*) &s_rd[wave][16 * t + 4 * g];
+                    const float rd[4] = {rd4.x, rd4.y, rd4.z, rd4.w};
+#pragma unroll
+                    for (int tj = 0; tj < NTT; ++tj)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            acc[t][tj][i] += rd[i] * tacc[t][tj][i];
+                            tacc[t][tj][i] = 0.f;
+                        }
+                }
+            }
+            if (c + 1 < nchunks) {
+                if constexpr (NB == 1) __syncthreads();  // every wave is done with the single activation tile
+                wave_lds_order();                        // this wave is done with its raw slab and factor rows
+                stage(NB == 2 ? (c + 1) & 1 : 0);
+                if (c + 2 < nchunks) fetch(c + 2);
+                __syncthreads();
             }
         }
-        __syncthreads();  // the tiles are consumed before the next chunk overwrites them
-    }
 
-    // out: row 4 lg + i of tile ti, token lr of tile tj
+        // out: weight row 16 t + 4 g + i of the wave, token 16 tj + lr
 #pragma unroll
-    for (int tj = 0; tj < 2; ++tj) {
-        const int tok = 32 * wc + 16 * tj + lr;
-        if (tok < nrows) {
-            const int64_t drow = ids ? ids[row0 + tok] : row0 + tok;
+        for (int tj = 0; tj < NTT; ++tj) {
+            const int tok = 16 * tj + lr;
+            if (tok < nrows) {
+                const int64_t drow = ids ? ids[row0 + tok] : row0 + tok;
+                float* o = dst + drow * ld_dst + (int64_t) bx * BM + 32 * wave + 4 * g;
 #pragma unroll
-            for (int ti = 0; ti < 2; ++ti)
+                for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    dst[drow * ld_dst + (int64_t) bx * kBM + 32 * wr + 16 * ti + 4 * lg + i] = acc[ti][tj][i];
+                    for (int i = 0; i < 4; ++i) o[16 * t + i] = acc[t][tj][i];
+            }
         }
-    }
+    };
+    if (ntt == 1) run(std::integral_constant<int, 1>{});
+    else if (ntt == 2) run(std::integral_constant<int, 2>{});
+    else if (ntt == 3) run(std::integral_constant<int, 3>{});
+    else run(std::integral_constant<int, 4>{});
 }
 
 __global__ void __launch_bounds__(kThreads) mmq_swiglu_kernel(const float* __restrict__ gu, float* __restrict__ h,
@@ -406,15 +647,24 @@ TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
     if (p->n == 0 || p->w_rows == 0) return TSX_OK;
     const MmqPlanes P = planes((void*) p->xq, p->total_rows, p->w_cols);
     const hipStream_t s = (hipStream_t) stream;
-    // the int8-MFMA tiles where the shape fits them, else the row-dot kernel
-    if (p->w_cols % kChunk == 0 && p->w_rows % kBM == 0 && p->n <= kMaxExpertsMmq && aligned(p->w, 16) &&
+    // the f16-MFMA tiles where the shape fits them (rows in multiples of 64), else the row-dot kernel
+    if (p->w_cols % kChunk == 0 && p->w_rows % 64 == 0 && p->n <= kMaxExpertsMmq && aligned(p->w, 16) &&
         p->expert_bytes % 16 == 0) {
         const int64_t max_tiles = (p->total_rows + kBN - 1) / kBN + p->n;
+        const int nw = p->w_rows % 256 == 0 ? 8 : p->w_rows % 128 == 0 ? 4 : 2;
         return with_type(p->type, [&](auto T) {
-            const dim3 grid((unsigned) (p->w_rows / kBM), (unsigned) max_tiles);
-            mmq_mfma_kernel<decltype(T)::value><<<grid, 256, 0, s>>>((const uint8_t*) p->w, p->expert_bytes, rb,
-                                                                     (int) p->w_cols, p->n, P, p->bounds, p->ids,
-                                                                     p->dst, p->ld_dst);
+            constexpr int TT = decltype(T)::value;
+            const dim3 grid((unsigned) (p->w_rows / (32 * nw)), (unsigned) max_tiles);
+            const uint8_t* w = (const uint8_t*) p->w;
+            if (nw == 8)
+                mmq_f16_kernel<TT, 8><<<grid, 512, 0, s>>>(w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds,
+                                                           p->ids, p->dst, p->ld_dst);
+            else if (nw == 4)
+                mmq_f16_kernel<TT, 4><<<grid, 256, 0, s>>>(w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds,
+                                                           p->ids, p->dst, p->ld_dst);
+            else
+                mmq_f16_kernel<TT, 2><<<grid, 128, 0, s>>>(w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds,
+                                                           p->ids, p->dst, p->ld_dst);
             return launch_status("tsx_moe_mmq_run/mfma");
         });
     }
