@@ -70,6 +70,9 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true", help="launch each step eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="before the timed region, run one plain fp32 copy kernel (out = in * 1) over this many MiB: "
+                         "the known-size launch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU; --gpus N > 1 is not supported (the sharding plan is design only)",
@@ -139,6 +142,16 @@ def main() -> int:
             graph.replay()
     torch.cuda.synchronize()
 
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib << 18  # fp32 elements
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"bench: copy probe read {4 * n} bytes and wrote {4 * n} bytes")
+        del src, dst
+
     # ---------------------------------------------------------------- timed region
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -163,7 +176,7 @@ def main() -> int:
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     if prefill:
-        # the grouped gate/up product (int8 MFMA) of every layer, on the current stream
+        # the grouped gate/up product (f16 MFMA on exact integer codes) of every layer, on the current stream
         def dom():
             for ml in mls:
                 W = ml.W
@@ -173,7 +186,7 @@ def main() -> int:
         dom_bytes = float(np.mean([n * gu_bytes + ml.n_ent * (N + N // 32 * 8) + ml.n_ent * 2 * FF * 4
                                    for n, ml in zip(distinct_per_layer, mls)]))
         dom_ops = 2.0 * T * k * 2 * FF * N
-        kernel = "mmq_mfma_kernel (grouped gate/up product, v_mfma_i32_16x16x32_i8) per layer"
+        kernel = "mmq_f16_kernel (grouped gate/up product, v_mfma_f32_16x16x32_f16 on exact integer codes) per layer"
     else:
         # the whole expert work of a layer: tsx_moe_decode_layer's two launches, on the current stream
         def dom():
@@ -185,9 +198,22 @@ def main() -> int:
         kernel = "tsx_moe_decode_layer (layer_gu_kernel + layer_down_kernel) per layer"
     dom()
     torch.cuda.synchronize()
+    # replayed from a HIP graph like the timed steps, so the figure is the kernels' time, not host launch gaps
+    dom_graph = None
+    if not args.eager:
+        s2 = torch.cuda.Stream()
+        s2.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s2):
+            dom()
+        torch.cuda.current_stream().wait_stream(s2)
+        dom_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(dom_graph):
+            dom()
+        dom_graph.replay()
+    torch.cuda.synchronize()
     ev0.record()
     for _ in range(reps):
-        dom()
+        dom_graph.replay() if dom_graph is not None else dom()
     ev1.record()
     torch.cuda.synchronize()
     dom_s = ev0.elapsed_time(ev1) / (reps * layers) / 1e3
@@ -199,7 +225,7 @@ def main() -> int:
     else:
         roof = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved_gbs / HBM_PEAK_GBS, 4)}
-    roof.update({"traffic": None, "kernel": kernel, "launch_us": round(dom_s * 1e6, 3),
+    roof.update({"traffic": measured_traffic(args.config), "kernel": kernel, "launch_us": round(dom_s * 1e6, 3),
                  "bytes_per_launch": int(dom_bytes), "int8_ops_per_launch": int(dom_ops),
                  "hbm_frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                  "int8_mfma_frac": round(achieved_tops / INT8_PEAK_TOPS, 4)})
@@ -240,6 +266,16 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def measured_traffic(config: str):
+    """HBM bytes per dominant launch from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE), each scaled by what the
+    same counter read for a copy kernel of known size; recorded in profiles/traffic.json.  None when not measured."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    rec = json.loads(f.read_text()).get(config)
+    return None if rec is None else rec.get("hbm_bytes_per_launch")
 
 
 def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared):
