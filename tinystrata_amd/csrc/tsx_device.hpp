@@ -25,6 +25,13 @@ constexpr int kWave = 64;
 
 // 16 bytes as one vector: what the 128-bit global and LDS loads move
 typedef int v4i __attribute__((ext_vector_type(4)));
+// a pointer into LDS: accesses through it are ds_read / ds_write even where the compiler cannot tell a generic
+// pointer's target (a flat access counts against vmcnt and waits behind the wave's global loads)
+template <typename T> using lds_ptr = __attribute__((address_space(3))) T*;
+// a pointer into global memory, for addresses computed through integers: loads through it are global_load, not flat
+// (a flat load also counts against lgkmcnt, so every later LDS wait would wait for it)
+template <typename T> using gbl_ptr = __attribute__((address_space(1))) T*;
+template <typename T> __device__ __forceinline__ gbl_ptr<const T> gbl_at(uintptr_t a) { return (gbl_ptr<const T>) a; }
 
 // ------------------------------------------------------------------ codebooks and sign tables, built at compile time
 // A sign entry turns 8 signs into what negates the matching bytes of two grid words: w = (g ^ mask) + (mask & 0x01..),
@@ -419,54 +426,52 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 // ------------------------------------------------------------------ routing of one token by one wave
 // Reference route_topk<NE,K> (src/kernels/cuda/native_router.cu:42-95): softmax with the max subtracted and one
 // reciprocal of the sum, NaN probabilities as -FLT_MAX, k rounds of argmax (ties to the lower id), weights divided by
-// max(sum of the picks, 6.1035e-5).  Expert e = lane + 64 i; n_expert a multiple of 64 up to kMaxExperts.  Each round
-// takes the wave's largest probability key, then the lowest id holding it (two DPP reductions); the pick's key then
-// drops below every other.
+// max(sum of the picks, 6.1035e-5).  Expert e = lane + 64 i; n_expert a multiple of 64 up to kMaxExperts (V = n_expert
+// / 64 columns, a template argument).  Each round takes the wave's largest probability key (a DPP reduction), then the
+// lowest id holding it from one ballot per column (the first column with a match, its lowest lane); the pick's key
+// then drops below every other.
 // ids / wts may point to global memory or LDS; every lane of the wave must call.
 constexpr int kMaxExperts = 512;
-__device__ __forceinline__ void route_token(const float* __restrict__ l, int n_expert, int k, int lane, int32_t* ids,
-                                            float* wts) {
-    constexpr int VM = kMaxExperts / 64;
-    const int V = n_expert / 64;
-    float v[VM];
+template <int V>
+__device__ __forceinline__ void route_token_v(const float* __restrict__ l, int k, int lane, int32_t* ids, float* wts) {
+    float v[V];
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < VM; ++i) {  // unconditional (clamped) loads keep the wait counts exact
-        const float li = l[lane + 64 * min(i, V - 1)];
-        v[i] = i < V ? li : -INFINITY;
+    for (int i = 0; i < V; ++i) {
+        v[i] = l[lane + 64 * i];
         mx = __builtin_fmaxf(mx, v[i]);
     }
     mx = reduce64(mx, OpMax());
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < VM; ++i) {
-        v[i] = i < V ? expf(v[i] - mx) : 0.f;
+    for (int i = 0; i < V; ++i) {
+        v[i] = expf(v[i] - mx);
         sum += v[i];
     }
     const float rcp = 1.0f / reduce64(sum, OpAddF());
-    uint32_t key[VM];
+    uint32_t key[V];
 #pragma unroll
-    for (int i = 0; i < VM; ++i) {
+    for (int i = 0; i < V; ++i) {
         float p = v[i] * rcp;
         if (__builtin_isnan(p)) p = -FLT_MAX;
-        key[i] = i < V ? ord_key(p) : 0u;  // 0: below every probability, -inf included
+        key[i] = ord_key(p);
     }
     float sel_sum = 0.f, my_p = 0.f;
     int my_id = 0;
     for (int r = 0; r < k; ++r) {
-        // each lane's best (key, lowest id among equal keys), the wave's largest key, then the lowest id holding it
+        // the wave's largest key, then the lowest id holding it: the first column with a match, its lowest lane
         uint32_t m = key[0];
-        int bi = 0;
 #pragma unroll
-        for (int i = 1; i < VM; ++i) {
-            const bool better = key[i] > m;
-            m = better ? key[i] : m;
-            bi = better ? i : bi;
-        }
+        for (int i = 1; i < V; ++i) m = max(m, key[i]);
         const uint32_t wm = wave_max_u32(m);
-        const int x = (int) wave_min_u32(m == wm ? (uint32_t) (lane + 64 * bi) : 0xFFFFFFFFu);
+        int x = -1;
 #pragma unroll
-        for (int i = 0; i < VM; ++i)
+        for (int i = 0; i < V; ++i) {
+            const uint64_t mask = __ballot(key[i] == wm);
+            if (x < 0 && mask != 0) x = 64 * i + __builtin_ctzll(mask);
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i)
             if (i == (x >> 6) && lane == (x & 63)) key[i] = 0u;  // drops below every other key
         const float p = key_value(wm);
         sel_sum += p;
@@ -479,6 +484,19 @@ __device__ __forceinline__ void route_token(const float* __restrict__ l, int n_e
     if (lane < k) {
         ids[lane] = my_id;
         wts[lane] = my_p * inv;
+    }
+}
+__device__ __forceinline__ void route_token(const float* __restrict__ l, int n_expert, int k, int lane, int32_t* ids,
+                                            float* wts) {
+    switch (n_expert / 64) {
+        case 1: route_token_v<1>(l, k, lane, ids, wts); break;
+        case 2: route_token_v<2>(l, k, lane, ids, wts); break;
+        case 3: route_token_v<3>(l, k, lane, ids, wts); break;
+        case 4: route_token_v<4>(l, k, lane, ids, wts); break;
+        case 5: route_token_v<5>(l, k, lane, ids, wts); break;
+        case 6: route_token_v<6>(l, k, lane, ids, wts); break;
+        case 7: route_token_v<7>(l, k, lane, ids, wts); break;
+        default: route_token_v<8>(l, k, lane, ids, wts); break;
     }
 }
 

@@ -93,14 +93,15 @@ struct LayerArgs {
 
 // one Q8_1 activation unit (32 codes + scale) from LDS planes (codes row-major, one float scale per 32)
 __device__ __forceinline__ void act_planes(const int8_t* codes, const float* d, Act& a) {
-    const v4i* p = (const v4i*) codes;
+    // the pointers are generic; the casts keep the reads ds_read (a flat load would wait behind the global loads)
+    const lds_ptr<const v4i> p = (lds_ptr<const v4i>) codes;
     const v4i q0 = p[0], q1 = p[1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         a.q[i] = q0[i];
         a.q[4 + i] = q1[i];
     }
-    a.d = *d;
+    a.d = *(lds_ptr<const float>) d;
 }
 
 // the Q8_1 code of v in a block whose largest magnitude is amax (scale d = q8_1_finite(amax / 127)): the codes of
@@ -229,7 +230,8 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     const int j = blockIdx.x;                      // slice: rows [32 j, 32 j + 32)
     v4i reg[kWLoadsA];
     auto issue = [&](int c) {
-        const v4i* src = (const v4i*) (blob + (w_up ? L.up_off : 0) + (uint64_t) (kSliceA * j + c * rows_c + wr0) * gu_row);
+        const gbl_ptr<const v4i> src =
+            gbl_at<v4i>((uintptr_t) (blob + (w_up ? L.up_off : 0) + (uint64_t) (kSliceA * j + c * rows_c + wr0) * gu_row));
 #pragma unroll
         for (int i = 0; i < kWLoadsA; ++i)  // unconditional (clamped) loads keep the wait counts exact
             reg[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, np - 1));
@@ -380,7 +382,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     const int wave = tid >> 6, lane = tid & 63;
     v4i reg[kWLoadsB];
     auto issue = [&](int un) {
-        const v4i* src = (const v4i*) (s_gsrc[un / halves] + (uint64_t) (un % halves) * rb * d_row);
+        const gbl_ptr<const v4i> src = gbl_at<v4i>((uintptr_t) (s_gsrc[un / halves] + (uint64_t) (un % halves) * rb * d_row));
 #pragma unroll
         for (int i = 0; i < kWLoadsB; ++i)  // unconditional (clamped) loads keep the wait counts exact
             reg[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, npu - 1));
