@@ -151,20 +151,39 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     const tsx_expert_layout L = a.L;
     const int N = (int) L.n_embd, NU = N / 32, FF = (int) L.n_ff;
 
-    // 0. what does not depend on the routing is requested first: the codebooks and, when they fit in registers,
-    //    every token's activations
+    // 0. what does not depend on the routing is requested first: the codebooks and, by the waves that do not route,
+    //    the first round of every token's activations
     uint32_t gw[GW > 0 ? GW : 1];
     if constexpr (GW > 0) grid_fetch<GT, GW>(gw, tid, kThreadsA);
     const int nq_all = T * N / 4;
-    const bool x_early = nq_all <= kThreadsA * kXLoads;
+    const int xt = tid - 64 * T, nxt = kThreadsA - 64 * T;  // the waves that do not route (T <= 8 of 16 route)
+    const float4* x4 = (const float4*) a.x;
     float4 xv[kXLoads];
-    if (x_early) {
 #pragma unroll
-        for (int i = 0; i < kXLoads; ++i) xv[i] = ((const float4*) a.x)[min(tid + kThreadsA * i, nq_all - 1)];
-    }
+    for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(max(xt, 0) + nxt * i, nq_all - 1)];
+    int8_t* s_xq = (int8_t*) (smem + kSlabA);
+    float* s_xd = (float*) (s_xq + T * N);
 
-    // 1. routing (one wave per token) and grouping, identical in every block
-    if (wave < T) route_token(a.logits + (int64_t) wave * a.n_expert, a.n_expert, k, lane, s_ids + wave * k, s_wts + wave * k);
+    // 1. routing (one wave per token) while the other waves quantize every token's activations to Q8_1 planes in
+    //    LDS (row t: token t); then grouping, identical in every block
+    if (wave < T) {
+        route_token(a.logits + (int64_t) wave * a.n_expert, a.n_expert, k, lane, s_ids + wave * k, s_wts + wave * k);
+    } else {
+        for (int base = 0; base < nq_all; base += nxt * kXLoads) {
+            if (base > 0) {
+#pragma unroll
+                for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(base + xt + nxt * i, nq_all - 1)];
+            }
+#pragma unroll
+            for (int i = 0; i < kXLoads; ++i) {
+                const int qd = base + xt + nxt * i;
+                if (base + nxt * i < nq_all)  // the same for every thread of these waves
+                    q8_1_quad_to_lds(xv[i], qd < nq_all, s_xq + 4 * qd, s_xd + qd / 8, xt & 7);
+            }
+        }
+    }
+    GridRef grid = grid_const();
+    if constexpr (GW > 0) grid = grid_store<GT, GW>(s_grid, gw, tid, kThreadsA);
     __syncthreads();
     if (wave == 0) {  // rank of entry `lane` in (expert, entry) order
         const int e = lane;
@@ -239,36 +258,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     v4i* wslab = (v4i*) smem + wave * (kSlabA / 16 / kWavesA);
     issue(0);
 
-    // Q8_1 planes of the activations: every token's (row t) when they were prefetched, else the block's entries'
-    // tokens (row c = entry p0 + c)
-    int8_t* s_xq = (int8_t*) (smem + kSlabA);
-    float* s_xd = (float*) (s_xq + T * N);
-    if (x_early) {
-#pragma unroll
-        for (int i = 0; i < kXLoads; ++i)
-            if (kThreadsA * i < nq_all)  // the same for every thread of the block
-                q8_1_quad_to_lds(xv[i], tid + kThreadsA * i < nq_all, s_xq + 4 * (tid + kThreadsA * i),
-                                 s_xd + (tid + kThreadsA * i) / 8, tid & 7);
-    } else {
-        const int nq = n_e * N / 4;  // quads of activation values; 8 consecutive lanes hold one Q8_1 block
-        for (int base = 0; base < nq; base += kThreadsA * kXLoads) {
-#pragma unroll
-            for (int i = 0; i < kXLoads; ++i) {
-                const int qc = min(base + tid + kThreadsA * i, nq - 1);
-                const int c = (4 * qc) / N, col = 4 * qc - c * N;
-                const int t = is_shared ? c : s_pos_ent[p0 + c] / k;
-                xv[i] = *(const float4*) (a.x + (int64_t) t * N + col);
-            }
-#pragma unroll
-            for (int i = 0; i < kXLoads; ++i) {
-                const int qd = base + tid + kThreadsA * i;
-                if (base + kThreadsA * i < nq) q8_1_quad_to_lds(xv[i], qd < nq, s_xq + 4 * qd, s_xd + qd / 8, tid & 7);
-            }
-        }
-    }
-    if (tid < n_e) s_xrow[tid] = x_early ? (is_shared ? tid : s_pos_ent[p0 + tid] / k) : tid;  // entry c's LDS row
-    GridRef grid = grid_const();
-    if constexpr (GW > 0) grid = grid_store<GT, GW>(s_grid, gw, tid, kThreadsA);
+    if (tid < n_e) s_xrow[tid] = is_shared ? tid : s_pos_ent[p0 + tid] / k;  // entry c's LDS row: its token
     __syncthreads();  // activations and codebooks are in LDS
 
     // 3. each chunk: the wave's rows into its LDS slab, then against every entry, tpr lanes per row
