@@ -51,12 +51,11 @@ constexpr int kSliceA = 32;           // gate (and up) rows per block of launch 
 constexpr int kSlabA = 64 * 1024;     // LDS bytes of a chunk of gate + up rows: 4 KB per wave
 constexpr int kWLoadsA = kSlabA / kWavesA / 16 / 64;  // 16-byte loads per lane of a wave's rows
 constexpr int kXLoads = 2;            // activation quads per thread per round of launch A
-constexpr int kThreadsB = 512;
-constexpr int kWavesB = kThreadsB / 64;
+constexpr int kThreadsB = 1024;
 constexpr int kRowsB = 8;             // output rows per block of launch B
-constexpr int kWLoadsB = 6;           // 16-byte loads per lane of a wave's rows (4 or 8 rows of one group)
-constexpr int kWaveSlabB = kWLoadsB * 64 * 16;
-constexpr int kHLoads = 6;            // 16-byte pieces of h per thread prefetched by launch B
+constexpr int kSlabB = 64 * 1024;     // LDS bytes of a chunk of groups' down rows (8 rows of each)
+constexpr int kBLoads = kSlabB / 16 / kThreadsB;  // 16-byte loads per thread in flight: a whole chunk
+constexpr int kHLoads = 3;            // 16-byte pieces of h per thread prefetched by launch B
 static_assert(kMaxTok <= kThreadsA / 64, "one wave per token in the routing");
 
 // the tables launch A leaves for launch B, at the start of the scratch buffer
@@ -318,6 +317,10 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
 }
 
 // ------------------------------------------------------------------ launch B
+// Block b owns output rows [8 b, 8 b + 8).  It reads the tables and every entry's h in one round trip, then loads the
+// 8 rows of every used expert's down matrix (and the shared expert's: 8 contiguous rows each) into LDS with every
+// thread's loads in flight at once (chunks of groups when they exceed the slab), dots each row with its group's
+// entries (tpr lanes per row, as many rows at once as the block has lanes for) and combines in pick order.
 template <int DT>
 __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
 #pragma clang fp contract(off)
@@ -364,24 +367,22 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     auto grp_lo = [&](int g) { return g < ng ? s_tab.grp_start[g] : n_ent; };
     auto grp_hi = [&](int g) { return g < ng ? s_tab.grp_start[g + 1] : n_ent + T; };
 
-    // work units: rb consecutive rows of one group (4, or 8 where 4 rows are not a whole number of 16-byte
-    // pieces); wave w takes units w, w + 8, ... and is the only reader of its LDS copy of them
-    const int rb = (4 * d_row) % 16 == 0 ? 4 : 8;
-    const int halves = kRowsB / rb, U = G * halves;
-    const int npu = (int) (rb * d_row / 16);  // 16-byte pieces of a unit (<= 64 * kWLoadsB)
-    const int wave = tid >> 6, lane = tid & 63;
-    v4i reg[kWLoadsB];
-    auto issue = [&](int un) {
-        const gbl_ptr<const v4i> src = gbl_at<v4i>((uintptr_t) (s_gsrc[un / halves] + (uint64_t) (un % halves) * rb * d_row));
+    // the groups' rows in chunks of gpc groups, every piece of a chunk in flight at once
+    const int gb = (int) (kRowsB * d_row), ppg = gb / 16;  // bytes and 16-byte pieces of a group's 8 rows
+    const int gpc = max(1, kSlabB / gb), nchunks = (G + gpc - 1) / gpc;
+    v4i reg[kBLoads];
+    auto issue = [&](int ch) {
+        const int g0 = ch * gpc, np = min(gpc, G - g0) * ppg;
 #pragma unroll
-        for (int i = 0; i < kWLoadsB; ++i)  // unconditional (clamped) loads keep the wait counts exact
-            reg[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, npu - 1));
+        for (int i = 0; i < kBLoads; ++i) {  // unconditional (clamped) loads keep the wait counts exact
+            const int q = min(tid + kThreadsB * i, np - 1), g = q / ppg, pp = q - g * ppg;
+            reg[i] = __builtin_nontemporal_load(gbl_at<v4i>((uintptr_t) s_gsrc[g0 + g]) + pp);
+        }
     };
-    v4i* wslab = (v4i*) (smem + (size_t) wave * kWaveSlabB);
-    if (wave < U) issue(wave);
+    issue(0);
 
     // h into LDS: the prefetched pieces, then any rest
-    int8_t* s_hq = (int8_t*) (smem + (size_t) kWavesB * kWaveSlabB);
+    int8_t* s_hq = (int8_t*) (smem + kSlabB);
     float* s_hd = (float*) (s_hq + (size_t) P * FF);
     v4i* hdst = (v4i*) s_hq;
 #pragma unroll
@@ -390,45 +391,58 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     for (int idx = tid + kThreadsB * kHLoads; idx < nh; idx += kThreadsB) hdst[idx] = hsrc[idx];
     GridRef grid = grid_const();
     if constexpr (GW > 0) grid = grid_store<DT, GW>(s_grid, gw, tid, kThreadsB);
-    __syncthreads();  // h and codebooks are in LDS
 
-    const int tpr = 64 / rb;  // lanes per row: 16 or 8
-    const int lr = lane / tpr, l = lane % tpr;
-    const uint8_t* row = (const uint8_t*) wslab + (uint64_t) lr * d_row;
-    for (int un = wave; un < U; un += kWavesB) {
+    v4i* slab = (v4i*) smem;
+    for (int ch = 0; ch < nchunks; ++ch) {
+        const int g0 = ch * gpc, gn = min(gpc, G - g0), np = gn * ppg;
 #pragma unroll
-        for (int i = 0; i < kWLoadsB; ++i)
-            if (lane + 64 * i < npu) wslab[lane + 64 * i] = reg[i];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's LDS writes land before its reads
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        if (un + kWavesB < U) issue(un + kWavesB);
-        const int g = un / halves, r = (un % halves) * rb + lr;
-        const int q0 = grp_lo(g), q1 = grp_hi(g);
-        for (int e0 = q0; e0 < q1; e0 += kNC) {
-            const int n = min(kNC, q1 - e0);
-            float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
-            for (int u = l; u < NUd; u += tpr) {
-                Unit w;
-                unit_load<DT>(row, u, w, grid);
+        for (int i = 0; i < kBLoads; ++i)
+            if (tid + kThreadsB * i < np) slab[tid + kThreadsB * i] = reg[i];
+        for (int q = tid + kThreadsB * kBLoads; q < np; q += kThreadsB) {  // a chunk larger than the loads in flight
+            const int g = q / ppg, pp = q - g * ppg;
+            slab[q] = gbl_at<v4i>((uintptr_t) s_gsrc[g0 + g])[pp];
+        }
+        __syncthreads();  // the chunk (and h, the codebooks) are in LDS
+        if (ch + 1 < nchunks) issue(ch + 1);
+        // rows ri = g * 8 + r of the chunk, tpr lanes each (consecutive lanes; tpr divides 64), in passes of
+        // kThreadsB / tpr rows when the chunk has more
+        const int R = gn * kRowsB;
+        int tpr = 64;
+        while (tpr > 4 && R * tpr > kThreadsB) tpr >>= 1;
+        const int l = tid % tpr;
+        for (int ri = tid / tpr; ri < R; ri += kThreadsB / tpr) {
+            const int g = ri / kRowsB, rr = ri % kRowsB;
+            const uint8_t* row = (const uint8_t*) smem + g * gb + rr * d_row;
+            const int q0 = grp_lo(g0 + g), q1 = grp_hi(g0 + g);
+            for (int e0 = q0; e0 < q1; e0 += kNC) {
+                const int n = min(kNC, q1 - e0);
+                float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
+                for (int u = l; u < NUd; u += tpr) {
+                    Unit w;
+                    unit_load<DT>(row, u, w, grid);
 #pragma unroll
-                for (int cc = 0; cc < kNC; ++cc) {
-                    if (cc < n) {
-                        Act xa;
-                        act_planes(s_hq + (size_t) (e0 + cc) * FF + 32 * u, s_hd + (e0 + cc) * NUd + u, xa);
-                        int S, M;
-                        acc[cc] += unit_dot<DT>(w, xa, S, M);
+                    for (int cc = 0; cc < kNC; ++cc) {
+                        if (cc < n) {
+                            Act xa;
+                            act_planes(s_hq + (size_t) (e0 + cc) * FF + 32 * u, s_hd + (e0 + cc) * NUd + u, xa);
+                            int S, M;
+                            acc[cc] += unit_dot<DT>(w, xa, S, M);
+                        }
                     }
                 }
+                switch (tpr) {
+                    case 4: sum_acc<4>(acc); break;
+                    case 8: sum_acc<8>(acc); break;
+                    case 16: sum_acc<16>(acc); break;
+                    case 32: sum_acc<32>(acc); break;
+                    default: sum_acc<64>(acc); break;
+                }
+                if (l == 0)
+                    for (int cc = 0; cc < n; ++cc) s_part[e0 + cc][rr] = acc[cc];
             }
-            if (tpr == 16) sum_acc<16>(acc);
-            else sum_acc<8>(acc);
-            if (l == 0)
-                for (int cc = 0; cc < n; ++cc) s_part[e0 + cc][r] = acc[cc];
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's reads are done before the next unit
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        __syncthreads();  // the chunk's rows are done before the next chunk overwrites the slab
     }
-    __syncthreads();
 
     // combine in pick order (tsx_moe_combine's arithmetic), into y
     if (tid < T * kRowsB) {
@@ -468,7 +482,7 @@ size_t lds_a(const tsx_expert_layout& L, int n_tok) {
 size_t lds_b(const tsx_expert_layout& L, int n_tok, int k, bool shared) {
     const int P = n_tok * k + (shared ? n_tok : 0);
     (void) L;
-    return (size_t) kWavesB * kWaveSlabB + (size_t) P * L.n_ff + (size_t) P * (L.n_ff / 32) * 4;
+    return (size_t) kSlabB + (size_t) P * L.n_ff + (size_t) P * (L.n_ff / 32) * 4;
 }
 size_t h_bytes(int n_tok, int k, int64_t n_ff) {  // codes then scales, the whole [n_tok * k + n_tok] positions
     const size_t P = (size_t) (n_tok * k + n_tok);
@@ -511,8 +525,7 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
         return TSX_ERR_UNSUPPORTED;
     }
     const int rows_c = pick_rows_c(L);
-    const uint64_t rb = (4 * L.d_row) % 16 == 0 ? 4 : 8;
-    if (rows_c == 0 || (rb * L.d_row) % 16 != 0 || rb * L.d_row > (uint64_t) kWaveSlabB || L.up_off % 16 != 0 ||
+    if (rows_c == 0 || (kRowsB * L.d_row) % 16 != 0 || kRowsB * L.d_row > (uint64_t) kSlabB || L.up_off % 16 != 0 ||
         L.down_off % 16 != 0 || lds_a(L, n_tok) > kMaxDynLds || lds_b(L, n_tok, k, shared != nullptr) > kMaxDynLds) {
         set_error("tsx_moe_decode_layer: row sizes (%llu, %llu) do not tile into 16-byte LDS slabs",
                   (unsigned long long) L.gu_row, (unsigned long long) L.d_row);
