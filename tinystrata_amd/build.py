@@ -41,6 +41,10 @@ COMMON = [
     "-Wno-unused-function",
     # packed fp32 arithmetic stays off on this pool (its packed forms have given wrong results)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # no merging of narrow loads into misaligned wide ones: GGUF fields sit on 2-byte boundaries, and a misaligned
+    # ds_read_b32/b64 measured ~1000 cycles per dependent read with 16 waves on gfx950 against ~130 for the aligned
+    # 16-bit reads it replaces
+    "-Xclang", "-target-feature", "-Xclang", "-unaligned-access-mode",
 ]
 
 
