@@ -102,7 +102,7 @@ def test_group_tables_exact(n_tok, k, E):
     assert (host(ed) == eed).all() and (host(et) == eet).all()
 
 
-@pytest.mark.parametrize("n_tok,k,E", [(512, 8, 128), (4096, 8, 256), (3, 2, 64)])
+@pytest.mark.parametrize("n_tok,k,E", [(512, 8, 128), (4096, 8, 256), (3, 2, 64), (129, 8, 512)])
 def test_route_sort_exact(n_tok, k, E):
     rng = np.random.default_rng(n_tok + E)
     bias = np.log(1.0 / (1 + rng.permutation(E)) ** 1.2)          # Zipf-skewed loads
@@ -114,10 +114,11 @@ def test_route_sort_exact(n_tok, k, E):
     assert (host(ri) == eri).all() and int(host(mr)[0]) == emr
 
 
+@pytest.mark.parametrize("n", [2048, 2046])   # four columns per thread, and the one-column form
 @pytest.mark.parametrize("shared", [False, True])
-def test_combine(shared):
+def test_combine(shared, n):
     rng = np.random.default_rng(3)
-    T, k, n = 4, 8, 2048
+    T, k = 4, 8
     parts = rng.normal(0, 1, (T * k, n)).astype(np.float32)
     wts = rng.random((T, k)).astype(np.float32)
     x = rng.normal(0, 1, (T, n)).astype(np.float32)

@@ -82,69 +82,95 @@ __global__ void __launch_bounds__(256) group_kernel(const int32_t* __restrict__ 
     }
 }
 
-// the prompt sort: counts, scan, then a stable scatter (16 waves per tile, per-wave counts committed in order)
+// the prompt sort, one block per tile of 1024 entries and no workspace: every block counts every entry (per expert:
+// all of them, and those of the tiles before its own), scans the totals into bounds, then scatters its own tile
+// stably - lanes of a wave that share an expert found with ballots, per-wave counts committed in wave order.
 constexpr int kSortThreads = 1024, kSortWaves = kSortThreads / 64;
+// the lanes of the wave holding the same expert as this lane (x = -1 for none): a mask over the wave
+__device__ __forceinline__ uint64_t same_expert(int x) {
+    uint64_t same = __ballot(1);
+#pragma unroll
+    for (int b = 0; b < 10; ++b) {  // experts < 512 (and -1) take 10 bits
+        const uint64_t bits = __ballot((x >> b) & 1);
+        same &= ((x >> b) & 1) ? bits : ~bits;
+    }
+    return same;
+}
 __global__ void __launch_bounds__(kSortThreads) route_sort_kernel(const int32_t* __restrict__ ids, int n_ent, int k,
                                                                   int n_expert, int32_t* __restrict__ bounds,
                                                                   int32_t* __restrict__ ent_dst, int32_t* __restrict__ ent_tok,
                                                                   int32_t* __restrict__ rinv, int32_t* __restrict__ max_rows) {
-    __shared__ int cnt[kMaxExperts], cur[kMaxExperts];
+    __shared__ int cnt[kMaxExperts], before[kMaxExperts], start[kMaxExperts];
     __shared__ int wcnt[kSortWaves][kMaxExperts];
-    __shared__ int s_max;
-    for (int x = threadIdx.x; x < n_expert; x += blockDim.x) cnt[x] = 0;
-    if (threadIdx.x == 0) s_max = 0;
+    __shared__ int s_wsum[kSortWaves], s_wmax[kSortWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile0 = blockIdx.x * kSortThreads;
+    for (int x = tid; x < n_expert; x += kSortThreads) cnt[x] = before[x] = 0;
+    for (int i = tid; i < kSortWaves * n_expert; i += kSortThreads) wcnt[i / n_expert][i % n_expert] = 0;
     __syncthreads();
-    for (int e = threadIdx.x; e < n_ent; e += blockDim.x) {
-        const int x = ids[e];
-        if (x >= 0 && x < n_expert) atomicAdd(&cnt[x], 1);  // an id out of range is dropped
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int pos = 0, mx = 0;
-        for (int x = 0; x < n_expert; ++x) {
-            bounds[x] = pos;
-            cur[x] = pos;
-            pos += cnt[x];
-            mx = max(mx, cnt[x]);
-        }
-        bounds[n_expert] = pos;
-        s_max = mx;
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int base = 0; base < n_ent; base += kSortThreads) {
-        for (int i = threadIdx.x; i < kSortWaves * n_expert; i += kSortThreads) wcnt[i / n_expert][i % n_expert] = 0;
-        __syncthreads();
-        const int e = base + threadIdx.x;
+    for (int base = 0; base < n_ent; base += kSortThreads) {  // a wave's 64 entries lie in one tile
+        const int e = base + tid;
         int x = e < n_ent ? ids[e] : -1;
-        if (x < 0 || x >= n_expert) x = -1;
-        uint64_t same = __ballot(1);
-#pragma unroll
-        for (int b = 0; b < 10; ++b) {
-            const uint64_t bits = __ballot((x >> b) & 1);
-            same &= ((x >> b) & 1) ? bits : ~bits;
+        if (x < 0 || x >= n_expert) x = -1;  // an id out of range is dropped
+        const uint64_t same = same_expert(x);
+        if (x >= 0 && __builtin_popcountll(same & ((1ull << lane) - 1ull)) == 0) {
+            const int c = __builtin_popcountll(same);
+            atomicAdd(&cnt[x], c);
+            if (base < tile0) atomicAdd(&before[x], c);
         }
-        const int rank = __builtin_popcountll(same & ((1ull << lane) - 1ull));
-        if (x >= 0 && rank == 0) wcnt[wave][x] = __builtin_popcountll(same);
-        __syncthreads();
-        for (int xx = threadIdx.x; xx < n_expert; xx += kSortThreads) {  // exclusive scan over the waves
-            int run = cur[xx];
-            for (int w = 0; w < kSortWaves; ++w) {
-                const int c = wcnt[w][xx];
-                wcnt[w][xx] = run;
-                run += c;
-            }
-            cur[xx] = run;
-        }
-        __syncthreads();
-        if (x >= 0) {
-            const int r = wcnt[wave][x] + rank;
-            ent_dst[r] = e;
-            ent_tok[r] = e / k;
-            rinv[e] = r;
-        }
-        __syncthreads();
     }
-    if (threadIdx.x == 0) *max_rows = s_max;
+    __syncthreads();
+    // bounds: exclusive scan of the counts over experts (expert x = thread x), and the largest count
+    {
+        const int v = tid < n_expert ? cnt[tid] : 0;
+        int inc = v, mx = v;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += t;
+            mx = max(mx, __shfl_xor(mx, o, 64));
+        }
+        if (lane == 63) s_wsum[wave] = inc;
+        if (lane == 0) s_wmax[wave] = mx;
+        __syncthreads();
+        int off = 0, total = 0, gmax = 0;
+        for (int w = 0; w < kSortWaves; ++w) {
+            off += w < wave ? s_wsum[w] : 0;
+            total += s_wsum[w];
+            gmax = max(gmax, s_wmax[w]);
+        }
+        if (tid < n_expert) {
+            start[tid] = off + inc - v + before[tid];  // this tile's first row of expert tid
+            if (blockIdx.x == 0) bounds[tid] = off + inc - v;
+        }
+        if (blockIdx.x == 0 && tid == 0) {
+            bounds[n_expert] = total;
+            *max_rows = gmax;
+        }
+    }
+    // this tile's entries, stably
+    const int e = tile0 + tid;
+    int x = e < n_ent ? ids[e] : -1;
+    if (x < 0 || x >= n_expert) x = -1;
+    const uint64_t same = same_expert(x);
+    const int rank = __builtin_popcountll(same & ((1ull << lane) - 1ull));
+    if (x >= 0 && rank == 0) wcnt[wave][x] = __builtin_popcountll(same);
+    __syncthreads();
+    for (int xx = tid; xx < n_expert; xx += kSortThreads) {  // exclusive scan over the waves
+        int run = start[xx];
+        for (int w = 0; w < kSortWaves; ++w) {
+            const int c = wcnt[w][xx];
+            wcnt[w][xx] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    if (x >= 0) {
+        const int r = wcnt[wave][x] + rank;
+        ent_dst[r] = e;
+        ent_tok[r] = e / k;
+        rinv[e] = r;
+    }
 }
 
 // x[t][i] += sum_j w_j parts[p(t,j)][i] (first product, then FMA, pick order) + sigmoid(sgate) * shared[t][i]
@@ -165,6 +191,38 @@ __global__ void __launch_bounds__(256) combine_kernel(float* __restrict__ x, con
         acc += gs * shared[(int64_t) t * n + i];
     }
     x[(int64_t) t * n + i] += acc;
+}
+
+// the same, four columns per thread (n a multiple of 4, every row 16-byte aligned)
+__global__ void __launch_bounds__(256) combine4_kernel(float* __restrict__ x, const float* __restrict__ parts,
+                                                       const int32_t* __restrict__ prow, const float* __restrict__ wts,
+                                                       int k, const float* __restrict__ shared,
+                                                       const float* __restrict__ sgate, int sg_stride, int n) {
+#pragma clang fp contract(off)
+    const int t = blockIdx.y;
+    const int i = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= n) return;
+    const float* wr = wts + (int64_t) t * k;
+    auto part = [&](int j) {
+        return *(const float4*) (parts + (int64_t) (prow ? prow[t * k + j] : t * k + j) * n + i);
+    };
+    float4 p = part(0);
+    const float w0 = wr[0];
+    float4 acc = {w0 * p.x, w0 * p.y, w0 * p.z, w0 * p.w};
+    for (int j = 1; j < k; ++j) {
+        p = part(j);
+        const float wj = wr[j];
+        acc = {__builtin_fmaf(wj, p.x, acc.x), __builtin_fmaf(wj, p.y, acc.y), __builtin_fmaf(wj, p.z, acc.z),
+               __builtin_fmaf(wj, p.w, acc.w)};
+    }
+    if (shared) {
+        const float gs = 1.0f / (1.0f + expf(-sgate[(int64_t) t * sg_stride]));
+        const float4 sh = *(const float4*) (shared + (int64_t) t * n + i);
+        acc = {acc.x + gs * sh.x, acc.y + gs * sh.y, acc.z + gs * sh.z, acc.w + gs * sh.w};
+    }
+    float4* xo = (float4*) (x + (int64_t) t * n + i);
+    const float4 xv = *xo;
+    *xo = float4{xv.x + acc.x, xv.y + acc.y, xv.z + acc.z, xv.w + acc.w};
 }
 
 }  // namespace
@@ -209,8 +267,9 @@ TSX_API int tsx_moe_route_sort(const int32_t* ids, int n_ent, int k, int n_exper
     }
     TSX_REQUIRE(ids && bounds && ent_dst && ent_tok && rinv && max_rows && n_ent >= 0 && k >= 1,
                 "tsx_moe_route_sort: a null pointer or a bad count");
-    route_sort_kernel<<<1, kSortThreads, 0, (hipStream_t) stream>>>(ids, n_ent, k, n_expert, bounds, ent_dst, ent_tok,
-                                                                    rinv, max_rows);
+    const unsigned tiles = (unsigned) std::max(1, (n_ent + kSortThreads - 1) / kSortThreads);
+    route_sort_kernel<<<tiles, kSortThreads, 0, (hipStream_t) stream>>>(ids, n_ent, k, n_expert, bounds, ent_dst,
+                                                                        ent_tok, rinv, max_rows);
     return launch_status("tsx_moe_route_sort");
 }
 
@@ -219,6 +278,11 @@ TSX_API int tsx_moe_combine(float* x, const float* parts, const int32_t* prow, c
     TSX_REQUIRE(x && parts && wts && k >= 1 && n >= 0 && n_tok >= 0 && (!shared || sgate),
                 "tsx_moe_combine: x, parts, wts, k >= 1 (and sgate with shared)");
     if (n == 0 || n_tok == 0) return TSX_OK;
+    if (n % 4 == 0 && aligned(x, 16) && aligned(parts, 16) && (!shared || aligned(shared, 16))) {
+        combine4_kernel<<<dim3((unsigned) ((n / 4 + 255) / 256), (unsigned) n_tok), 256, 0, (hipStream_t) stream>>>(
+            x, parts, prow, wts, k, shared, sgate, sg_stride, n);
+        return launch_status("tsx_moe_combine");
+    }
     combine_kernel<<<dim3((unsigned) ((n + 255) / 256), (unsigned) n_tok), 256, 0, (hipStream_t) stream>>>(
         x, parts, prow, wts, k, shared, sgate, sg_stride, n);
     return launch_status("tsx_moe_combine");
