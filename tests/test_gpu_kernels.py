@@ -136,12 +136,15 @@ def test_combine(shared, n):
         assert (got == exp).all()
 
 
-def test_mmq_quantize_planes_exact():
+@pytest.mark.parametrize("pad", [0, 1])  # rows 16-byte aligned (four values per lane), and not (one per lane)
+def test_mmq_quantize_planes_exact(pad):
     rng = np.random.default_rng(8)
     rows, cols = 70, 512
-    x = rng.normal(0, 1, (100, cols)).astype(np.float32)
+    xw = rng.normal(0, 1, (100, cols + pad)).astype(np.float32)
+    xw[3, 32:64] = 0.0                               # an all-zero block
+    x = xw[:, :cols]
     ids = rng.integers(0, 100, rows).astype(np.int32)
-    xq = host(ops.mmq_quantize(dev(x), dev(ids), Q4_K, cols, cols, rows))
+    xq = host(ops.mmq_quantize(dev(xw), dev(ids), Q4_K, cols, cols + pad, rows))
     rp = (rows + 63) // 64 * 64 + 64
     r256 = lambda v: (v + 255) // 256 * 256
     q = xq[: rp * cols].view(np.int8).reshape(rp, cols)

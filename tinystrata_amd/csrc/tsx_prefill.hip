@@ -39,9 +39,41 @@ __host__ __device__ inline MmqPlanes planes(void* base, int64_t rows, int64_t co
     return p;
 }
 
-// one 32-lane group per Q8_1 block: row i of the output is row ids[i] (or i) of x
+// 8 lanes per Q8_1 block, 4 values each (float4 loads, 4-byte code stores, DPP reductions within the 8 lanes):
+// row i of the output is row ids[i] (or i) of x.  The codes of q8_1_store32, byte for byte.
 __global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __restrict__ x, const int32_t* __restrict__ ids,
                                                                 MmqPlanes P, int64_t cols, int64_t ld, int64_t rows) {
+    const int64_t nq = cols / 4;  // quads per row
+    const int64_t qi = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const bool valid = qi < rows * nq;
+    const int64_t qc = valid ? qi : rows * nq - 1;  // every lane takes part in the reductions
+    const int64_t i = qc / nq, c4 = qc % nq;
+    const int64_t src = ids ? ids[i] : i;
+    const float4 v = *(const float4*) (x + src * ld + 4 * c4);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = lanes_reduce<8>(amax, OpMax());
+    const float d = q8_1_finite(amax / 127.0f);
+    auto code = [&](float f) {
+        if (amax == 0.0f) return 0;
+        const float r = roundf(f / d);
+        return (int) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
+    };
+    const int q0 = code(v.x), q1 = code(v.y), q2 = code(v.z), q3 = code(v.w);
+    const float qs = lanes_reduce<8>((float) (q0 + q1 + q2 + q3), OpAddF());  // |sum| <= 32 * 127: exact in fp32
+    if (valid) {
+        *(uint32_t*) (P.q + i * cols + 4 * c4) = ((uint32_t) q0 & 0xFFu) | ((uint32_t) q1 & 0xFFu) << 8 |
+                                                 ((uint32_t) q2 & 0xFFu) << 16 | ((uint32_t) q3 & 0xFFu) << 24;
+        if ((c4 & 7) == 0) {
+            const int64_t b = c4 / 8;
+            P.d[i * (cols / 32) + b] = h2f(f2h(q8_1_finite(d)));
+            P.m[i * (cols / 32) + b] = (int32_t) qs;
+        }
+    }
+}
+
+// the same for rows that are not 16-byte aligned: one 32-lane group per Q8_1 block, one value per lane
+__global__ void __launch_bounds__(kThreads) mmq_quantize1_kernel(const float* __restrict__ x, const int32_t* __restrict__ ids,
+                                                                 MmqPlanes P, int64_t cols, int64_t ld, int64_t rows) {
     const int64_t nb = cols / 32;
     const int64_t gi = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) / 32;
     const int lane = threadIdx.x & 31;
@@ -625,8 +657,15 @@ TSX_API int tsx_moe_mmq_quantize(const float* x, const int32_t* ids, void* xq, i
     const MmqPlanes P = planes(xq, rows, cols);
     const hipStream_t s = (hipStream_t) stream;
     if (rows > 0) {
-        const int64_t threads = rows * (cols / 32) * 32;
-        mmq_quantize_kernel<<<(unsigned) ((threads + kThreads - 1) / kThreads), kThreads, 0, s>>>(x, ids, P, cols, ld, rows);
+        if (aligned(x, 16) && ld % 4 == 0) {
+            const int64_t threads = rows * (cols / 4);
+            mmq_quantize_kernel<<<(unsigned) ((threads + kThreads - 1) / kThreads), kThreads, 0, s>>>(x, ids, P, cols, ld,
+                                                                                                      rows);
+        } else {
+            const int64_t threads = rows * (cols / 32) * 32;
+            mmq_quantize1_kernel<<<(unsigned) ((threads + kThreads - 1) / kThreads), kThreads, 0, s>>>(x, ids, P, cols, ld,
+                                                                                                       rows);
+        }
         const int rc = launch_status("tsx_moe_mmq_quantize");
         if (rc != TSX_OK) return rc;
     }
