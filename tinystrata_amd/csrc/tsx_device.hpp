@@ -78,61 +78,69 @@ struct GridRef {
     const SignEntry* s_sign;
 };
 __device__ __forceinline__ GridRef grid_const() { return GridRef{kGrid.xxs, kGrid.s, kGrid.xxs_sign, kGrid.s_sign}; }
-// LDS words the tables of weight type T take (0 for types without a codebook)
-template <int T>
-constexpr int grid_lds_words() {
-    return T == TSX_IQ3_XXS ? 256 + 2 * 128 : T == TSX_IQ3_S ? 512 + 2 * 256 : 0;
+// Bank-private copies of T's tables in LDS.  Lanes of a wave pick codebook entries at random, so one shared copy
+// makes them collide in the LDS banks (several passes per read); with R copies of each entry, entry i's copy for
+// lane l at slot i * R + l % R, lanes l and l' < R apart always read different banks.  The sign entries of IQ3_S
+// are copied fewer times so that both tables, the weight slab and the activations fit one block's LDS.
+template <int T> constexpr int rep_grid_copies() { return T == TSX_IQ3_XXS ? 32 : T == TSX_IQ3_S ? 16 : 0; }
+template <int T> constexpr int rep_sign_copies() { return T == TSX_IQ3_XXS ? 32 : T == TSX_IQ3_S ? 16 : 0; }
+template <int T> constexpr int rep_grid_entries() { return T == TSX_IQ3_XXS ? 256 : T == TSX_IQ3_S ? 512 : 0; }
+template <int T> constexpr int rep_sign_entries() { return T == TSX_IQ3_XXS ? 128 : T == TSX_IQ3_S ? 256 : 0; }
+template <int T> constexpr int rep_grid_bytes() { return rep_grid_entries<T>() * rep_grid_copies<T>() * 4; }
+// LDS bytes of the copies (0 for formats without a codebook); a multiple of 16
+template <int T> constexpr int rep_lds_bytes() { return rep_grid_bytes<T>() + rep_sign_entries<T>() * rep_sign_copies<T>() * 8; }
+// the 16-byte stores that fill the copies: four copies of a grid word, or two of a sign entry, each
+template <int T> constexpr int rep_stores() {
+    return rep_grid_entries<T>() * rep_grid_copies<T>() / 4 + rep_sign_entries<T>() * rep_sign_copies<T>() / 2;
 }
-// the words of T's tables this thread copies (up to PER of them; word i = tid + n * k), loaded from the constant
-// tables: issue early, store later with grid_store
+// what a lane reads the copies through: its own slot of every entry
+template <int T>
+struct RepTab {
+    const uint32_t* grid;
+    const uint64_t* sign;
+};
+// the values this thread stores (store q = tid + n * k), requested from the constant tables: issue early, store
+// later with rep_store.  PER >= rep_stores<T>() / n.
 template <int T, int PER>
-__device__ __forceinline__ void grid_fetch(uint32_t (&w)[PER], int tid, int n) {
-    constexpr int W = grid_lds_words<T>();
-    const uint32_t* src = T == TSX_IQ3_XXS ? kGrid.xxs : kGrid.s;
-    const uint32_t* sgn = (const uint32_t*) (T == TSX_IQ3_XXS ? kGrid.xxs_sign : kGrid.s_sign);
-    constexpr int G = T == TSX_IQ3_XXS ? 256 : 512;
+__device__ __forceinline__ void rep_fetch(uint64_t (&v)[PER], int tid, int n) {
+    constexpr int NG = rep_grid_entries<T>() * rep_grid_copies<T>() / 4, NS = rep_stores<T>() - NG;
+    const uint32_t* g = T == TSX_IQ3_XXS ? kGrid.xxs : kGrid.s;
+    const uint64_t* sg = (const uint64_t*) (T == TSX_IQ3_XXS ? kGrid.xxs_sign : kGrid.s_sign);
 #pragma unroll
     for (int k = 0; k < PER; ++k) {  // unconditional (clamped) loads keep the wait counts exact
-        const int i = min(tid + n * k, W - 1);
-        w[k] = i < G ? src[i] : sgn[i - G];
+        const int q = min(tid + n * k, NG + NS - 1);
+        v[k] = q < NG ? (uint64_t) g[q * 4 / rep_grid_copies<T>()] : sg[(q - NG) * 2 / rep_sign_copies<T>()];
     }
 }
 template <int T, int PER>
-__device__ __forceinline__ GridRef grid_store(uint32_t* lds, const uint32_t (&w)[PER], int tid, int n) {
-    constexpr int W = grid_lds_words<T>();
-    constexpr int G = T == TSX_IQ3_XXS ? 256 : 512;
+__device__ __forceinline__ RepTab<T> rep_store(uint8_t* lds, const uint64_t (&v)[PER], int tid, int n) {
+    constexpr int NG = rep_grid_entries<T>() * rep_grid_copies<T>() / 4, NS = rep_stores<T>() - NG;
+    const lds_ptr<v4i> dst = (lds_ptr<v4i>) lds;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int i = tid + n * k;
-        if (i < W) lds[i] = w[k];
+        const int q = tid + n * k;
+        const int lo = (int) (uint32_t) v[k], hi = (int) (uint32_t) (v[k] >> 32);
+        if (q < NG) dst[q] = v4i{lo, lo, lo, lo};
+        else if (q < NG + NS) dst[q] = v4i{lo, hi, lo, hi};
     }
-    GridRef r = grid_const();
-    if (T == TSX_IQ3_XXS) {
-        r.xxs = lds;
-        r.xxs_sign = (const SignEntry*) (lds + G);
-    } else if (T == TSX_IQ3_S) {
-        r.s = lds;
-        r.s_sign = (const SignEntry*) (lds + G);
-    }
-    return r;
+    const int lane = __lane_id();
+    return RepTab<T>{(const uint32_t*) lds + lane % max(rep_grid_copies<T>(), 1),
+                     (const uint64_t*) (lds + rep_grid_bytes<T>()) + lane % max(rep_sign_copies<T>(), 1)};
 }
-// copies T's tables into LDS with the block's threads; the caller synchronizes before use
-template <int T>
-__device__ __forceinline__ GridRef grid_to_lds(uint32_t* lds, int tid, int n) {
-    constexpr int W = grid_lds_words<T>();
-    constexpr int G = T == TSX_IQ3_XXS ? 256 : 512;
-    const uint32_t* src = T == TSX_IQ3_XXS ? kGrid.xxs : kGrid.s;
-    const uint32_t* sgn = (const uint32_t*) (T == TSX_IQ3_XXS ? kGrid.xxs_sign : kGrid.s_sign);
-    for (int i = tid; i < W; i += n) lds[i] = i < G ? src[i] : sgn[i - G];
-    GridRef r = grid_const();
-    if (T == TSX_IQ3_XXS) {
-        r.xxs = lds;
-        r.xxs_sign = (const SignEntry*) (lds + G);
-    } else if (T == TSX_IQ3_S) {
-        r.s = lds;
-        r.s_sign = (const SignEntry*) (lds + G);
-    }
-    return r;
+
+// table reads, by where the tables are: the constant tables (GridRef) or a lane's copies (RepTab)
+template <int T> __device__ __forceinline__ uint32_t tab_grid(const GridRef& g, uint32_t i) {
+    return T == TSX_IQ3_XXS ? g.xxs[i] : g.s[i];
+}
+template <int T> __device__ __forceinline__ SignEntry tab_sign(const GridRef& g, uint32_t i) {
+    return T == TSX_IQ3_XXS ? g.xxs_sign[i] : g.s_sign[i];
+}
+template <int T> __device__ __forceinline__ uint32_t tab_grid(const RepTab<T>& r, uint32_t i) {
+    return r.grid[i * rep_grid_copies<T>()];
+}
+template <int T> __device__ __forceinline__ SignEntry tab_sign(const RepTab<T>& r, uint32_t i) {
+    const uint64_t v = r.sign[i * rep_sign_copies<T>()];
+    return SignEntry{(uint32_t) v, (uint32_t) (v >> 32)};
 }
 
 // ------------------------------------------------------------------ scalar helpers
@@ -162,9 +170,9 @@ template <> struct Fmt<TSX_IQ3_S> { static constexpr int upb = 8, bytes = 110; }
 template <> struct Fmt<TSX_Q4_K> { static constexpr int upb = 8, bytes = 144; };
 template <> struct Fmt<TSX_Q8_0> { static constexpr int upb = 1, bytes = 34; };
 
-template <int T> __device__ __forceinline__ void unit_load(const uint8_t* row, int u, Unit& o, GridRef g);
 
-template <> __device__ __forceinline__ void unit_load<TSX_IQ3_XXS>(const uint8_t* row, int u, Unit& o, GridRef g) {
+template <typename Tab>
+__device__ __forceinline__ void unit_load_iq3xxs(const uint8_t* row, int u, Unit& o, const Tab& g) {
     const uint8_t* blk = row + (u >> 3) * 98;
     const int j = u & 7;
     const float d = h2f((uint16_t) ld16(blk));
@@ -172,17 +180,18 @@ template <> __device__ __forceinline__ void unit_load<TSX_IQ3_XXS>(const uint8_t
     const uint32_t aux = ld32a2(blk + 66 + 4 * j);
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-        const SignEntry sg = g.xxs_sign[(aux >> (7 * l)) & 127u];
+        const SignEntry sg = tab_sign<TSX_IQ3_XXS>(g, (aux >> (7 * l)) & 127u);
         const uint32_t q = l < 2 ? q0 : q1;
         const uint32_t i0 = (q >> (16 * (l & 1))) & 255u, i1 = (q >> (16 * (l & 1) + 8)) & 255u;
-        o.w[2 * l] = (int) apply_signs(g.xxs[i0], sg.mask_lo);
-        o.w[2 * l + 1] = (int) apply_signs(g.xxs[i1], sg.mask_hi);
+        o.w[2 * l] = (int) apply_signs(tab_grid<TSX_IQ3_XXS>(g, i0), sg.mask_lo);
+        o.w[2 * l + 1] = (int) apply_signs(tab_grid<TSX_IQ3_XXS>(g, i1), sg.mask_hi);
     }
     o.a = d * 0.25f * (float) (2 * (int) (aux >> 28) + 1);
     o.b = 0.f;
 }
 
-template <> __device__ __forceinline__ void unit_load<TSX_IQ3_S>(const uint8_t* row, int u, Unit& o, GridRef g) {
+template <typename Tab>
+__device__ __forceinline__ void unit_load_iq3s(const uint8_t* row, int u, Unit& o, const Tab& g) {
     const uint8_t* blk = row + (u >> 3) * 110;
     const int j = u & 7;
     const float d = h2f((uint16_t) ld16(blk));
@@ -192,19 +201,19 @@ template <> __device__ __forceinline__ void unit_load<TSX_IQ3_S>(const uint8_t* 
     const uint32_t sc = (blk[106 + (j >> 1)] >> (4 * (j & 1))) & 15u;
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
-        const SignEntry sg = g.s_sign[(sb >> (8 * l)) & 255u];
+        const SignEntry sg = tab_sign<TSX_IQ3_S>(g, (sb >> (8 * l)) & 255u);
         const uint32_t q = l < 2 ? q0 : q1;
         const int k0 = 2 * l, k1 = 2 * l + 1;
         const uint32_t i0 = ((q >> (8 * (k0 & 3))) & 255u) | (((qh >> k0) & 1u) << 8);
         const uint32_t i1 = ((q >> (8 * (k1 & 3))) & 255u) | (((qh >> k1) & 1u) << 8);
-        o.w[k0] = (int) apply_signs(g.s[i0], sg.mask_lo);
-        o.w[k1] = (int) apply_signs(g.s[i1], sg.mask_hi);
+        o.w[k0] = (int) apply_signs(tab_grid<TSX_IQ3_S>(g, i0), sg.mask_lo);
+        o.w[k1] = (int) apply_signs(tab_grid<TSX_IQ3_S>(g, i1), sg.mask_hi);
     }
     o.a = d * (float) (2 * (int) sc + 1);
     o.b = 0.f;
 }
 
-template <> __device__ __forceinline__ void unit_load<TSX_Q4_K>(const uint8_t* row, int u, Unit& o, GridRef g) {
+__device__ __forceinline__ void unit_load_q4k(const uint8_t* row, int u, Unit& o) {
     const uint8_t* blk = row + (u >> 3) * 144;
     const int j = u & 7;
     const float d = h2f((uint16_t) ld16(blk)), dmin = h2f((uint16_t) ld16(blk + 2));
@@ -225,13 +234,22 @@ template <> __device__ __forceinline__ void unit_load<TSX_Q4_K>(const uint8_t* r
     o.b = dmin * (float) m;
 }
 
-template <> __device__ __forceinline__ void unit_load<TSX_Q8_0>(const uint8_t* row, int u, Unit& o, GridRef g) {
+__device__ __forceinline__ void unit_load_q80(const uint8_t* row, int u, Unit& o) {
     const uint8_t* blk = row + u * 34;
     const float d = h2f((uint16_t) ld16(blk));
 #pragma unroll
     for (int k = 0; k < 8; ++k) o.w[k] = (int) ld32a2(blk + 2 + 4 * k);
     o.a = d;
     o.b = 0.f;
+}
+
+// unit u of a row of format T; g: where the codebooks are read (GridRef or RepTab<T>)
+template <int T, typename Tab>
+__device__ __forceinline__ void unit_load(const uint8_t* row, int u, Unit& o, const Tab& g) {
+    if constexpr (T == TSX_IQ3_XXS) unit_load_iq3xxs(row, u, o, g);
+    else if constexpr (T == TSX_IQ3_S) unit_load_iq3s(row, u, o, g);
+    else if constexpr (T == TSX_Q4_K) unit_load_q4k(row, u, o);
+    else unit_load_q80(row, u, o);
 }
 
 // one Q8_1 activation block: d and the 32 codes as 8 words

@@ -38,6 +38,7 @@
 #include "tsx_device.hpp"
 
 #include <climits>
+#include <type_traits>
 
 namespace tsx {
 namespace {
@@ -48,12 +49,12 @@ constexpr int kNC = 4;                // entries per pass over a row's units
 constexpr int kThreadsA = 1024;
 constexpr int kWavesA = kThreadsA / 64;
 constexpr int kSliceA = 32;           // gate (and up) rows per block of launch A: one Q8_1 block of h per entry
-constexpr int kSlabA = 64 * 1024;     // LDS bytes of a chunk of gate + up rows: 4 KB per wave
+constexpr int kSlabA = 64 * 1024;     // most LDS bytes of a chunk of gate + up rows: 4 KB per wave
 constexpr int kWLoadsA = kSlabA / kWavesA / 16 / 64;  // 16-byte loads per lane of a wave's rows
 constexpr int kXLoads = 2;            // activation quads per thread per round of launch A
 constexpr int kThreadsB = 1024;
 constexpr int kRowsB = 8;             // output rows per block of launch B
-constexpr int kSlabB = 64 * 1024;     // LDS bytes of a chunk of groups' down rows (8 rows of each)
+constexpr int kSlabB = 64 * 1024;     // most LDS bytes of a chunk of groups' down rows (8 rows of each)
 constexpr int kBLoads = kSlabB / 16 / kThreadsB;  // 16-byte loads per thread in flight: a whole chunk
 constexpr int kHLoads = 3;            // 16-byte pieces of h per thread prefetched by launch B
 static_assert(kMaxTok <= kThreadsA / 64, "one wave per token in the routing");
@@ -82,6 +83,7 @@ struct LayerArgs {
     const float* sgate;
     int sg_stride;
     int rows_c;                   // gate (and up) rows per chunk of launch A: 32, 16 or 8
+    int slab_a, slab_b;           // LDS bytes of the weight slabs (<= kSlabA, kSlabB: what the codebooks leave)
     float* y;
     int32_t* ids;
     float* wts;
@@ -135,9 +137,9 @@ __device__ __forceinline__ void sum_acc(float (&acc)[kNC]) {
 template <int GT>
 __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
 #pragma clang fp contract(off)
-    constexpr int GW = (grid_lds_words<GT>() + kThreadsA - 1) / kThreadsA;
+    constexpr int RP = (rep_stores<GT>() + kThreadsA - 1) / kThreadsA;
+    using Tab = std::conditional_t<(RP > 0), RepTab<GT>, GridRef>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ __attribute__((aligned(16))) uint32_t s_grid[GW > 0 ? GW * kThreadsA : 4];
     __shared__ int32_t s_ids[kMaxEnt], s_sorted[kMaxEnt], s_pos_ent[kMaxEnt], s_ent_pos[kMaxEnt];
     __shared__ int32_t s_grp_expert[kMaxEnt], s_grp_start[kMaxEnt + 1];
     __shared__ float s_wts[kMaxEnt];
@@ -152,15 +154,15 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
 
     // 0. what does not depend on the routing is requested first: the codebooks and, by the waves that do not route,
     //    the first round of every token's activations
-    uint32_t gw[GW > 0 ? GW : 1];
-    if constexpr (GW > 0) grid_fetch<GT, GW>(gw, tid, kThreadsA);
+    uint64_t rv[RP > 0 ? RP : 1];
+    if constexpr (RP > 0) rep_fetch<GT, RP>(rv, tid, kThreadsA);
     const int nq_all = T * N / 4;
     const int xt = tid - 64 * T, nxt = kThreadsA - 64 * T;  // the waves that do not route (T <= 8 of 16 route)
     const float4* x4 = (const float4*) a.x;
     float4 xv[kXLoads];
 #pragma unroll
     for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(max(xt, 0) + nxt * i, nq_all - 1)];
-    int8_t* s_xq = (int8_t*) (smem + kSlabA);
+    int8_t* s_xq = (int8_t*) (smem + a.slab_a + rep_lds_bytes<GT>());
     float* s_xd = (float*) (s_xq + T * N);
 
     // 1. routing (one wave per token) while the other waves quantize every token's activations to Q8_1 planes in
@@ -181,8 +183,9 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
             }
         }
     }
-    GridRef grid = grid_const();
-    if constexpr (GW > 0) grid = grid_store<GT, GW>(s_grid, gw, tid, kThreadsA);
+    Tab grid;
+    if constexpr (RP > 0) grid = rep_store<GT, RP>(smem + a.slab_a, rv, tid, kThreadsA);
+    else grid = grid_const();
     __syncthreads();
     if (wave == 0) {  // rank of entry `lane` in (expert, entry) order
         const int e = lane;
@@ -254,7 +257,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
         for (int i = 0; i < kWLoadsA; ++i)  // unconditional (clamped) loads keep the wait counts exact
             reg[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, np - 1));
     };
-    v4i* wslab = (v4i*) smem + wave * (kSlabA / 16 / kWavesA);
+    v4i* wslab = (v4i*) smem + wave * (a.slab_a / 16 / kWavesA);
     issue(0);
 
     if (tid < n_e) s_xrow[tid] = is_shared ? tid : s_pos_ent[p0 + tid] / k;  // entry c's LDS row: its token
@@ -324,9 +327,9 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
 template <int DT>
 __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
 #pragma clang fp contract(off)
-    constexpr int GW = (grid_lds_words<DT>() + kThreadsB - 1) / kThreadsB;
+    constexpr int RP = (rep_stores<DT>() + kThreadsB - 1) / kThreadsB;
+    using Tab = std::conditional_t<(RP > 0), RepTab<DT>, GridRef>;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ __attribute__((aligned(16))) uint32_t s_grid[GW > 0 ? GW * kThreadsB : 4];
     __shared__ LayerTables s_tab;
     __shared__ float s_part[kMaxEnt + kMaxTok][kRowsB];
     __shared__ const uint8_t* s_gsrc[kMaxEnt + 1];
@@ -341,8 +344,8 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
 
     // requested together: the codebooks, the tables and every entry's h (codes, then scales: contiguous in the
     // scratch, as in LDS), whose positions are fixed: n_tok * k routed, then n_tok shared
-    uint32_t gw[GW > 0 ? GW : 1];
-    if constexpr (GW > 0) grid_fetch<DT, GW>(gw, tid, kThreadsB);
+    uint64_t rv[RP > 0 ? RP : 1];
+    if constexpr (RP > 0) rep_fetch<DT, RP>(rv, tid, kThreadsB);
     const int P = n_ent + (a.shared ? T : 0);
     const int nh = (P * FF + P * NUd * 4) / 16;  // 16-byte pieces (n_ff is a multiple of 128)
     const v4i* hsrc = (const v4i*) a.hc;
@@ -369,7 +372,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
 
     // the groups' rows in chunks of gpc groups, every piece of a chunk in flight at once
     const int gb = (int) (kRowsB * d_row), ppg = gb / 16;  // bytes and 16-byte pieces of a group's 8 rows
-    const int gpc = max(1, kSlabB / gb), nchunks = (G + gpc - 1) / gpc;
+    const int gpc = max(1, a.slab_b / gb), nchunks = (G + gpc - 1) / gpc;
     v4i reg[kBLoads];
     auto issue = [&](int ch) {
         const int g0 = ch * gpc, np = min(gpc, G - g0) * ppg;
@@ -382,15 +385,16 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     issue(0);
 
     // h into LDS: the prefetched pieces, then any rest
-    int8_t* s_hq = (int8_t*) (smem + kSlabB);
+    int8_t* s_hq = (int8_t*) (smem + a.slab_b + rep_lds_bytes<DT>());
     float* s_hd = (float*) (s_hq + (size_t) P * FF);
     v4i* hdst = (v4i*) s_hq;
 #pragma unroll
     for (int i = 0; i < kHLoads; ++i)
         if (tid + kThreadsB * i < nh) hdst[tid + kThreadsB * i] = hv[i];
     for (int idx = tid + kThreadsB * kHLoads; idx < nh; idx += kThreadsB) hdst[idx] = hsrc[idx];
-    GridRef grid = grid_const();
-    if constexpr (GW > 0) grid = grid_store<DT, GW>(s_grid, gw, tid, kThreadsB);
+    Tab grid;
+    if constexpr (RP > 0) grid = rep_store<DT, RP>(smem + a.slab_b, rv, tid, kThreadsB);
+    else grid = grid_const();
 
     v4i* slab = (v4i*) smem;
     for (int ch = 0; ch < nchunks; ++ch) {
@@ -471,25 +475,31 @@ int with_type(int type, F&& f) {
 }
 
 // the largest rows_c in {32, 16, 8} whose gate + up chunk fits the slab with every wave's rows 16-byte aligned
-int pick_rows_c(const tsx_expert_layout& L) {
+int pick_rows_c(const tsx_expert_layout& L, int slab_a) {
     for (int rc = kSliceA; rc >= 8; rc >>= 1)
-        if (2 * rc * L.gu_row <= (uint64_t) kSlabA && ((2 * rc / kWavesA) * L.gu_row) % 16 == 0) return rc;
+        if (2 * rc * L.gu_row <= (uint64_t) slab_a && ((2 * rc / kWavesA) * L.gu_row) % 16 == 0) return rc;
     return 0;
 }
-size_t lds_a(const tsx_expert_layout& L, int n_tok) {
-    return (size_t) kSlabA + (size_t) n_tok * L.n_embd + (size_t) n_tok * (L.n_embd / 32) * 4;
+size_t rep_bytes(int type) {
+    return (size_t) with_type(type, [](auto T) { return rep_lds_bytes<decltype(T)::value>(); });
 }
-size_t lds_b(const tsx_expert_layout& L, int n_tok, int k, bool shared) {
+size_t x_planes_bytes(const tsx_expert_layout& L, int n_tok) {
+    return (size_t) n_tok * L.n_embd + (size_t) n_tok * (L.n_embd / 32) * 4;
+}
+size_t h_planes_bytes(const tsx_expert_layout& L, int n_tok, int k, bool shared) {
     const int P = n_tok * k + (shared ? n_tok : 0);
-    (void) L;
-    return (size_t) kSlabB + (size_t) P * L.n_ff + (size_t) P * (L.n_ff / 32) * 4;
+    return (size_t) P * L.n_ff + (size_t) P * (L.n_ff / 32) * 4;
+}
+// the largest slab (a multiple of `unit` bytes, at most `most`) that fits beside `fixed` bytes in `limit`
+int fit_slab(size_t limit, size_t fixed, int most, int unit) {
+    if (limit <= fixed) return 0;
+    return (int) std::min<size_t>((size_t) most, (limit - fixed) / unit * unit);
 }
 size_t h_bytes(int n_tok, int k, int64_t n_ff) {  // codes then scales, the whole [n_tok * k + n_tok] positions
     const size_t P = (size_t) (n_tok * k + n_tok);
     return P * (size_t) n_ff + P * (size_t) (n_ff / 32) * 4;
 }
 constexpr size_t kLdsPerWorkgroup = 160 * 1024;  // gfx950
-constexpr size_t kMaxDynLds = 140 * 1024;        // the most any launch here asks for (the checks below hold it)
 // lets a kernel take more than the default 64 KB of dynamic LDS: up to what its static LDS leaves of the 160 KB.
 // Returns that limit (0 when the runtime refused); once per kernel.
 size_t set_max_lds(const void* kern) {
@@ -524,11 +534,27 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
                   L.gu_type, L.d_type, (long long) L.n_embd, (long long) L.n_ff, n_tok, n_expert, k);
         return TSX_ERR_UNSUPPORTED;
     }
-    const int rows_c = pick_rows_c(L);
-    if (rows_c == 0 || (kRowsB * L.d_row) % 16 != 0 || kRowsB * L.d_row > (uint64_t) kSlabB || L.up_off % 16 != 0 ||
-        L.down_off % 16 != 0 || lds_a(L, n_tok) > kMaxDynLds || lds_b(L, n_tok, k, shared != nullptr) > kMaxDynLds) {
-        set_error("tsx_moe_decode_layer: row sizes (%llu, %llu) do not tile into 16-byte LDS slabs",
-                  (unsigned long long) L.gu_row, (unsigned long long) L.d_row);
+    // LDS of each launch: the weight slab, the codebook copies, the activations (x, or every entry's h); the slabs
+    // take what the rest leaves of each kernel's limit
+    size_t lim_a = 0, lim_b = 0;
+    with_type(L.gu_type, [&](auto T) {
+        static const size_t limit = set_max_lds((const void*) layer_gu_kernel<decltype(T)::value>);
+        lim_a = limit;
+        return 0;
+    });
+    with_type(L.d_type, [&](auto T) {
+        static const size_t limit = set_max_lds((const void*) layer_down_kernel<decltype(T)::value>);
+        lim_b = limit;
+        return 0;
+    });
+    const size_t fixed_a = rep_bytes(L.gu_type) + x_planes_bytes(L, n_tok);
+    const size_t fixed_b = rep_bytes(L.d_type) + h_planes_bytes(L, n_tok, k, shared != nullptr);
+    const int slab_a = fit_slab(lim_a, fixed_a, kSlabA, 16 * kWavesA), slab_b = fit_slab(lim_b, fixed_b, kSlabB, 16);
+    const int rows_c = pick_rows_c(L, slab_a);
+    if (rows_c == 0 || (kRowsB * L.d_row) % 16 != 0 || kRowsB * L.d_row > (uint64_t) slab_b || L.up_off % 16 != 0 ||
+        L.down_off % 16 != 0) {
+        set_error("tsx_moe_decode_layer: row sizes (%llu, %llu) do not tile into 16-byte LDS slabs of %d and %d bytes",
+                  (unsigned long long) L.gu_row, (unsigned long long) L.d_row, slab_a, slab_b);
         return TSX_ERR_UNSUPPORTED;
     }
     TSX_REQUIRE(blobs && logits && x && y && ids && wts && scratch && (!shared || sgate),
@@ -550,6 +576,8 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
     a.sgate = sgate;
     a.sg_stride = sg_stride;
     a.rows_c = rows_c;
+    a.slab_a = slab_a;
+    a.slab_b = slab_b;
     a.y = y;
     a.ids = ids;
     a.wts = wts;
@@ -560,12 +588,7 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
     const hipStream_t s = (hipStream_t) stream;
     int rc = with_type(L.gu_type, [&](auto T) {
         auto kern = layer_gu_kernel<decltype(T)::value>;
-        static const size_t limit = set_max_lds((const void*) kern);
-        const size_t lds = lds_a(L, n_tok);
-        if (lds > limit) {
-            set_error("tsx_moe_decode_layer: gate/up needs %zu B of LDS, %zu available", lds, limit);
-            return (int) TSX_ERR_UNSUPPORTED;
-        }
+        const size_t lds = (size_t) slab_a + fixed_a;
         const dim3 grid((unsigned) (L.n_ff / kSliceA), (unsigned) (a.cap_groups + (shared ? 1 : 0)));
         kern<<<grid, kThreadsA, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/gate-up");
@@ -573,12 +596,7 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
     if (rc != TSX_OK) return rc;
     return with_type(L.d_type, [&](auto T) {
         auto kern = layer_down_kernel<decltype(T)::value>;
-        static const size_t limit = set_max_lds((const void*) kern);
-        const size_t lds = lds_b(L, n_tok, k, shared != nullptr);
-        if (lds > limit) {
-            set_error("tsx_moe_decode_layer: down needs %zu B of LDS, %zu available", lds, limit);
-            return (int) TSX_ERR_UNSUPPORTED;
-        }
+        const size_t lds = (size_t) slab_b + fixed_b;
         kern<<<(unsigned) (L.n_embd / kRowsB), kThreadsB, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/down");
     });
