@@ -415,48 +415,56 @@ __device__ __forceinline__ void q8_1_store32(float x, tsx_block_q8_1* y, int i) 
 }
 
 
-// the wave's largest 32-bit unsigned value, the same in every lane (all 64 lanes active)
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, 0xF, 0xF, false);
+// the wave's largest (smallest) 32-bit unsigned value, the same in every lane (all 64 lanes active): four DPP steps
+// within each 16-lane row, two row broadcasts (lane 15 of rows 0 and 2 into rows 1 and 3, then lane 31 into rows 2
+// and 3), and lane 63 read out.  Lanes a step does not write keep `old`, the operation's identity.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v, uint32_t old = 0u) {
+    return (uint32_t) __builtin_amdgcn_update_dpp((int) old, (int) v, CTRL, ROWS, 0xF, false);
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, dpp_u32<0xB1>(v));
-    v = max(v, dpp_u32<0x4E>(v));
-    v = max(v, dpp_u32<0x141>(v));
-    v = max(v, dpp_u32<0x140>(v));
-    const uint32_t a = (uint32_t) __builtin_amdgcn_readlane((int) v, 15), b = (uint32_t) __builtin_amdgcn_readlane((int) v, 31);
-    const uint32_t c = (uint32_t) __builtin_amdgcn_readlane((int) v, 47), d = (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
-    return max(max(a, b), max(c, d));
+    v = max(v, dpp_u32<0xB1>(v));        // quad_perm [1,0,3,2]
+    v = max(v, dpp_u32<0x4E>(v));        // quad_perm [2,3,0,1]
+    v = max(v, dpp_u32<0x141>(v));       // row_half_mirror
+    v = max(v, dpp_u32<0x140>(v));       // row_mirror
+    v = max(v, dpp_u32<0x142, 0xA>(v));  // row_bcast:15
+    v = max(v, dpp_u32<0x143, 0xC>(v));  // row_bcast:31
+    return (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
 }
-
-// the wave's smallest 32-bit unsigned value, the same in every lane (all 64 lanes active)
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-    v = min(v, dpp_u32<0xB1>(v));
-    v = min(v, dpp_u32<0x4E>(v));
-    v = min(v, dpp_u32<0x141>(v));
-    v = min(v, dpp_u32<0x140>(v));
-    const uint32_t a = (uint32_t) __builtin_amdgcn_readlane((int) v, 15), b = (uint32_t) __builtin_amdgcn_readlane((int) v, 31);
-    const uint32_t c = (uint32_t) __builtin_amdgcn_readlane((int) v, 47), d = (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
-    return min(min(a, b), min(c, d));
+    constexpr uint32_t id = 0xFFFFFFFFu;
+    v = min(v, dpp_u32<0xB1>(v, id));
+    v = min(v, dpp_u32<0x4E>(v, id));
+    v = min(v, dpp_u32<0x141>(v, id));
+    v = min(v, dpp_u32<0x140>(v, id));
+    v = min(v, dpp_u32<0x142, 0xA>(v, id));
+    v = min(v, dpp_u32<0x143, 0xC>(v, id));
+    return (uint32_t) __builtin_amdgcn_readlane((int) v, 63);
 }
 
 // ------------------------------------------------------------------ routing of one token by one wave
 // Reference route_topk<NE,K> (src/kernels/cuda/native_router.cu:42-95): softmax with the max subtracted and one
 // reciprocal of the sum, NaN probabilities as -FLT_MAX, k rounds of argmax (ties to the lower id), weights divided by
 // max(sum of the picks, 6.1035e-5).  Expert e = lane + 64 i; n_expert a multiple of 64 up to kMaxExperts (V = n_expert
-// / 64 columns, a template argument).  Each round takes the wave's largest probability key (a DPP reduction), then the
-// lowest id holding it from one ballot per column (the first column with a match, its lowest lane); the pick's key
-// then drops below every other.
-// ids / wts may point to global memory or LDS; every lane of the wave must call.
+// / 64 columns, a template argument).  Each lane sorts its V keys; each round takes the wave's largest head (a DPP
+// reduction), then the lowest id holding it (from the one lane holding it, or a second reduction when heads are equal),
+// and the winning lane pops its head.
+// ids / wts may point to global memory or LDS; every lane of the wave must call.  route_fetch and route_select split
+// the routing so that a kernel can request the logits before anything else and wait for them alone.
 constexpr int kMaxExperts = 512;
+constexpr int kRouteV = kMaxExperts / 64;  // logits per lane
+__device__ __forceinline__ void route_fetch(const float* __restrict__ l, int n_expert, int lane, float (&v)[kRouteV]) {
+#pragma unroll
+    for (int i = 0; i < kRouteV; ++i)  // unconditional (clamped) loads keep the wait counts exact
+        v[i] = l[min(lane + 64 * i, n_expert - 1)];
+}
 template <int V>
-__device__ __forceinline__ void route_token_v(const float* __restrict__ l, int k, int lane, int32_t* ids, float* wts) {
+__device__ __forceinline__ void route_select_v(const float (&lv)[kRouteV], int k, int lane, int32_t* ids, float* wts) {
     float v[V];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-        v[i] = l[lane + 64 * i];
+        v[i] = lv[i];
         mx = __builtin_fmaxf(mx, v[i]);
     }
     mx = reduce64(mx, OpMax());
@@ -474,23 +482,41 @@ __device__ __forceinline__ void route_token_v(const float* __restrict__ l, int k
         if (__builtin_isnan(p)) p = -FLT_MAX;
         key[i] = ord_key(p);
     }
+    // each lane's keys sorted largest first, with their ids (a stable network: equal keys keep the lower id first);
+    // a round's winner pops its head
+    uint32_t id[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) id[i] = (uint32_t) (64 * i + lane);
+#pragma unroll
+    for (int i = 1; i < V; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j) {
+            const bool sw = key[j] > key[j - 1];
+            const uint32_t k0 = key[j - 1], k1 = key[j], i0 = id[j - 1], i1 = id[j];
+            key[j - 1] = sw ? k1 : k0;
+            key[j] = sw ? k0 : k1;
+            id[j - 1] = sw ? i1 : i0;
+            id[j] = sw ? i0 : i1;
+        }
     float sel_sum = 0.f, my_p = 0.f;
     int my_id = 0;
     for (int r = 0; r < k; ++r) {
-        // the wave's largest key, then the lowest id holding it: the first column with a match, its lowest lane
-        uint32_t m = key[0];
+        // the wave's largest head, then the lowest id holding it: read from the one lane holding it, or (equal heads
+        // in several lanes) the smallest of their ids
+        const uint32_t wm = wave_max_u32(key[0]);
+        const uint64_t hit = __ballot(key[0] == wm);
+        int x;
+        if (__builtin_popcountll(hit) == 1)
+            x = __builtin_amdgcn_readlane((int) id[0], (int) __builtin_ctzll(hit));
+        else
+            x = (int) wave_min_u32(key[0] == wm ? id[0] : 0xFFFFFFFFu);
+        const bool win = lane == (x & 63);
 #pragma unroll
-        for (int i = 1; i < V; ++i) m = max(m, key[i]);
-        const uint32_t wm = wave_max_u32(m);
-        int x = -1;
-#pragma unroll
-        for (int i = 0; i < V; ++i) {
-            const uint64_t mask = __ballot(key[i] == wm);
-            if (x < 0 && mask != 0) x = 64 * i + __builtin_ctzll(mask);
+        for (int i = 0; i + 1 < V; ++i) {
+            key[i] = win ? key[i + 1] : key[i];
+            id[i] = win ? id[i + 1] : id[i];
         }
-#pragma unroll
-        for (int i = 0; i < V; ++i)
-            if (i == (x >> 6) && lane == (x & 63)) key[i] = 0u;  // drops below every other key
+        key[V - 1] = win ? 0u : key[V - 1];  // below every other key
         const float p = key_value(wm);
         sel_sum += p;
         if (lane == r) {
@@ -504,18 +530,24 @@ __device__ __forceinline__ void route_token_v(const float* __restrict__ l, int k
         wts[lane] = my_p * inv;
     }
 }
+__device__ __forceinline__ void route_select(const float (&v)[kRouteV], int n_expert, int k, int lane, int32_t* ids,
+                                             float* wts) {
+    switch (n_expert / 64) {
+        case 1: route_select_v<1>(v, k, lane, ids, wts); break;
+        case 2: route_select_v<2>(v, k, lane, ids, wts); break;
+        case 3: route_select_v<3>(v, k, lane, ids, wts); break;
+        case 4: route_select_v<4>(v, k, lane, ids, wts); break;
+        case 5: route_select_v<5>(v, k, lane, ids, wts); break;
+        case 6: route_select_v<6>(v, k, lane, ids, wts); break;
+        case 7: route_select_v<7>(v, k, lane, ids, wts); break;
+        default: route_select_v<8>(v, k, lane, ids, wts); break;
+    }
+}
 __device__ __forceinline__ void route_token(const float* __restrict__ l, int n_expert, int k, int lane, int32_t* ids,
                                             float* wts) {
-    switch (n_expert / 64) {
-        case 1: route_token_v<1>(l, k, lane, ids, wts); break;
-        case 2: route_token_v<2>(l, k, lane, ids, wts); break;
-        case 3: route_token_v<3>(l, k, lane, ids, wts); break;
-        case 4: route_token_v<4>(l, k, lane, ids, wts); break;
-        case 5: route_token_v<5>(l, k, lane, ids, wts); break;
-        case 6: route_token_v<6>(l, k, lane, ids, wts); break;
-        case 7: route_token_v<7>(l, k, lane, ids, wts); break;
-        default: route_token_v<8>(l, k, lane, ids, wts); break;
-    }
+    float v[kRouteV];
+    route_fetch(l, n_expert, lane, v);
+    route_select(v, n_expert, k, lane, ids, wts);
 }
 
 }  // namespace tsx

@@ -152,8 +152,11 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     const tsx_expert_layout L = a.L;
     const int N = (int) L.n_embd, NU = N / 32, FF = (int) L.n_ff;
 
-    // 0. what does not depend on the routing is requested first: the codebooks and, by the waves that do not route,
-    //    the first round of every token's activations
+    // 0. the routing waves' logits are requested first (their wait then covers those loads alone), then what does
+    //    not depend on the routing: the codebooks and, by the waves that do not route, the first round of every
+    //    token's activations
+    float lg[kRouteV];
+    if (wave < T) route_fetch(a.logits + (int64_t) wave * a.n_expert, a.n_expert, lane, lg);
     uint64_t rv[RP > 0 ? RP : 1];
     if constexpr (RP > 0) rep_fetch<GT, RP>(rv, tid, kThreadsA);
     const int nq_all = T * N / 4;
@@ -168,7 +171,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     // 1. routing (one wave per token) while the other waves quantize every token's activations to Q8_1 planes in
     //    LDS (row t: token t); then grouping, identical in every block
     if (wave < T) {
-        route_token(a.logits + (int64_t) wave * a.n_expert, a.n_expert, k, lane, s_ids + wave * k, s_wts + wave * k);
+        route_select(lg, a.n_expert, k, lane, s_ids + wave * k, s_wts + wave * k);
     } else {
         for (int base = 0; base < nq_all; base += nxt * kXLoads) {
             if (base > 0) {
@@ -342,8 +345,10 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     const uint64_t d_row = L.d_row;
     const int r0 = blockIdx.x * kRowsB;
 
-    // requested together: the codebooks, the tables and every entry's h (codes, then scales: contiguous in the
-    // scratch, as in LDS), whose positions are fixed: n_tok * k routed, then n_tok shared
+    // requested together, the tables first (the first wait is for them alone): the tables, the codebooks and every
+    // entry's h (codes, then scales: contiguous in the scratch, as in LDS), whose positions are fixed: n_tok * k
+    // routed, then n_tok shared
+    const uint32_t tw = ((const uint32_t*) a.tab)[min(tid, kTableWords - 1)];
     uint64_t rv[RP > 0 ? RP : 1];
     if constexpr (RP > 0) rep_fetch<DT, RP>(rv, tid, kThreadsB);
     const int P = n_ent + (a.shared ? T : 0);
@@ -355,11 +360,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     const float sg = a.shared ? a.sgate[(int64_t) min(tid, T - 1) * a.sg_stride] : 0.f;
     const int ty = min(tid / kRowsB, T - 1), ry = tid % kRowsB;  // the y value this thread combines into
     const float y0 = a.y[(int64_t) ty * N + r0 + ry];
-    {
-        const uint32_t w = ((const uint32_t*) a.tab)[min(tid, kTableWords - 1)];
-        if (tid < kTableWords) ((uint32_t*) &s_tab)[tid] = w;
-        if (tid < T) s_sgate[tid] = sg;
-    }
+    if (tid < kTableWords) ((uint32_t*) &s_tab)[tid] = tw;
     __syncthreads();
     const int ng = s_tab.n_groups;
     const int G = ng + (a.shared ? 1 : 0);  // group ng is the shared expert: positions [n_ent, n_ent + T)
@@ -385,6 +386,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     issue(0);
 
     // h into LDS: the prefetched pieces, then any rest
+    if (tid < T) s_sgate[tid] = sg;
     int8_t* s_hq = (int8_t*) (smem + a.slab_b + rep_lds_bytes<DT>());
     float* s_hd = (float*) (s_hq + (size_t) P * FF);
     v4i* hdst = (v4i*) s_hq;
