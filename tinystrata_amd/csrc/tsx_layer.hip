@@ -12,17 +12,18 @@
 // weights; B: one table read -> weights) and issues everything else alongside, and cross-lane reductions use DPP
 // and readlane rather than LDS permutes.
 //
-// Launch A, grid (n_ff/32 slices, cap_groups [+1 for the shared expert]), 1024 threads.  Every block
-//   1. routes every token (route_token: one wave per token, the code of tsx_moe_router_topk) and groups the entries
-//      by expert in LDS (ascending id, entries in entry order); it takes group blockIdx.y, or the shared expert in
-//      the last block row;
-//   2. issues 16-byte loads of the slice's 32 gate rows and 32 up rows (contiguous in the blob; rows too long for
-//      one 64 KB LDS slab come in chunks, the next chunk's loads issued before the current one is computed), with
-//      the activations and codebooks requested at the start, and quantizes the activations to Q8_1 in LDS while
-//      the rows arrive;
-//   3. dots the rows with every entry (each unit decoded once for all entries), applies SwiGLU (the product rounded
-//      on its own) and writes the slice's Q8_1 block of h per entry.  Block (0, 0) also writes ids / wts and the
-//      tables launch B needs.
+// Launch A, 256 blocks (one per CU) of 1024 threads.  Every block
+//   1. routes every token (route_select: one wave per token, the code of tsx_moe_router_topk) and groups the entries
+//      by expert in LDS (ascending id, entries in entry order), while its other waves quantize the activations to
+//      Q8_1 in LDS;
+//   2. takes an equal run of the layer's slices (a slice: gate and up rows [32 j, 32 j + 32) of one group's expert;
+//      the groups' slices one after another, the shared expert's last), so every CU has the same rows however many
+//      groups the routing made;
+//   3. streams each slice's rows into wave-private LDS slabs with 16-byte loads (rows too long for one slab come in
+//      chunks; a wave requests its next chunk's rows before computing the current one), dots them with every entry
+//      of the slice's group (each unit decoded once for all entries), applies SwiGLU (the product rounded on its own)
+//      and writes the slice's Q8_1 block of h per entry.  Block 0 also writes ids / wts and the tables launch B
+//      needs.
 // Launch B, grid n_embd/8, 256 threads.  Every block owns 8 output rows: it reads the tables and every entry's h in
 //   one round trip, loads those 8 rows of every used expert's down matrix (and the shared expert's) into LDS,
 //   dots, and combines in pick order: y += w0*p0, fmaf(wj, pj, .) ..., + sigmoid(sgate)*shared -
@@ -48,7 +49,8 @@ constexpr int kMaxEnt = 64;           // routed entries (tokens x k)
 constexpr int kNC = 4;                // entries per pass over a row's units
 constexpr int kThreadsA = 1024;
 constexpr int kWavesA = kThreadsA / 64;
-constexpr int kSliceA = 32;           // gate (and up) rows per block of launch A: one Q8_1 block of h per entry
+constexpr int kSliceA = 32;           // gate (and up) rows of a launch A slice: one Q8_1 block of h per entry
+constexpr int kBlocksA = 256;         // launch A: one block per CU, each an equal run of slices
 constexpr int kSlabA = 64 * 1024;     // most LDS bytes of a chunk of gate + up rows: 4 KB per wave
 constexpr int kWLoadsA = kSlabA / kWavesA / 16 / 64;  // 16-byte loads per lane of a wave's rows
 constexpr int kXLoads = 2;            // activation quads per thread per round of launch A
@@ -76,13 +78,14 @@ struct LayerArgs {
     tsx_expert_layout L;
     const uint8_t* blobs;
     uint64_t stride;
-    int n_expert, k, n_tok, cap_groups;
+    int n_expert, k, n_tok;
     const float* logits;
     const float* x;
     const uint8_t* shared;
     const float* sgate;
     int sg_stride;
     int rows_c;                   // gate (and up) rows per chunk of launch A: 32, 16 or 8
+    int chunks_a;                 // chunks per slice: 32 / rows_c
     int slab_a, slab_b;           // LDS bytes of the weight slabs (<= kSlabA, kSlabB: what the codebooks leave)
     float* y;
     int32_t* ids;
@@ -127,10 +130,21 @@ __device__ __forceinline__ void q8_1_quad_to_lds(const float4& x, bool valid, in
     }
 }
 
+// x / d for 0 <= x < 2^22 and d >= 1, from rd ~ 1 / d (v_rcp_f32 is within an ulp): the float quotient is within one
+// of the truth (an integer division would put ~40 instructions on the path to the weight loads)
+__device__ __forceinline__ int div_small(int x, int d, float rd) {
+    int q = (int) ((float) x * rd);
+    q -= q * d > x ? 1 : 0;
+    q += (q + 1) * d <= x ? 1 : 0;
+    return q;
+}
+
+// the sums of the first nu accumulators over each W-lane row (nu the same in every lane of the wave)
 template <int W>
-__device__ __forceinline__ void sum_acc(float (&acc)[kNC]) {
+__device__ __forceinline__ void sum_acc(float (&acc)[kNC], int nu) {
 #pragma unroll
-    for (int c = 0; c < kNC; ++c) acc[c] = lanes_sum<W>(acc[c]);
+    for (int c = 0; c < kNC; ++c)
+        if (c < nu) acc[c] = lanes_sum<W>(acc[c]);
 }
 
 // ------------------------------------------------------------------ launch A
@@ -145,7 +159,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     __shared__ float s_wts[kMaxEnt];
     __shared__ int s_ngroups;
     __shared__ float s_gu[kMaxTok][2 * kSliceA];
-    __shared__ int s_xrow[kMaxTok];
+    __shared__ int s_prow[kMaxEnt + kMaxTok];  // position -> its token's activation row
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int T = a.n_tok, k = a.k, n_ent = T * k;
@@ -220,7 +234,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
     }
     __syncthreads();
     const int ng = s_ngroups;
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
+    if (blockIdx.x == 0) {
         if (tid < n_ent) {
             a.ids[tid] = s_ids[tid];
             a.wts[tid] = s_wts[tid];
@@ -234,91 +248,114 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
         if (tid == 0) a.tab->n_groups = ng;
     }
 
-    // this block's expert and entries
-    const int gy = blockIdx.y;
-    const bool is_shared = gy == a.cap_groups;
-    if (!is_shared && gy >= ng) return;  // the whole block: no group this far
-    const uint8_t* blob = is_shared ? a.shared : a.blobs + (uint64_t) s_grp_expert[gy] * a.stride;
-    const int p0 = is_shared ? n_ent : s_grp_start[gy];
-    const int n_e = is_shared ? T : s_grp_start[gy + 1] - p0;  // <= T: a token picks an expert once
+    // 2. this block's slices.  A slice is 32 pairs - gate rows and up rows [32 j, 32 j + 32) - of one group's expert:
+    //    one Q8_1 block of h per entry.  The groups' n_ff / 32 slices come one after another, the shared expert's
+    //    last, and every block takes an equal run of them, so every CU has the same rows however many groups the
+    //    routing made.
+    const int spg = FF / kSliceA, G = ng + (a.shared ? 1 : 0), total = G * spg, nb = (int) gridDim.x;
+    const float rspg = __builtin_amdgcn_rcpf((float) spg);
+    const int share = div_small(total + nb - 1, nb, __builtin_amdgcn_rcpf((float) nb));
+    const int s0 = (int) blockIdx.x * share, s1 = min(total, s0 + share);
+    if (s0 >= s1) return;  // the whole block: nothing this far
 
-    // 2. each wave's rows of the first chunk in flight, then the activations.  A chunk is 2 * rows_c rows (gate
+    // 3. each wave's rows of the first chunk in flight.  A slice comes in nchunks chunks of 2 * rows_c rows (gate
     //    rows, then up rows); wave w owns rpw of them and is the only reader of its LDS copy, so it starts computing
-    //    as soon as its own rows have arrived.
-    const int rows_c = a.rows_c, nchunks = kSliceA / rows_c;
+    //    as soon as its own rows have arrived, and requests the next chunk's (of this slice or the next) first.
+    const int rows_c = a.rows_c, nchunks = a.chunks_a;
     const int rpw = 2 * rows_c / kWavesA;          // rows per wave: 4, 2 or 1
     const bool w_up = wave >= kWavesA / 2;
     const int wr0 = rpw * (wave % (kWavesA / 2));  // the wave's first row within the chunk's gate (or up) rows
     const uint64_t gu_row = L.gu_row;
     const int np = (int) (rpw * gu_row / 16);      // 16-byte pieces of the wave's rows (<= 64 * kWLoadsA)
-    const int j = blockIdx.x;                      // slice: rows [32 j, 32 j + 32)
+    struct Slice {
+        const uint8_t* blob;
+        int p0, n_e, j;  // the group's first position and entry count (<= T: a token picks an expert once); slice j
+    };
+    auto slice_at = [&](int sl) {
+        const int g = div_small(sl, spg, rspg);
+        Slice r;
+        r.blob = g < ng ? a.blobs + (uint64_t) s_grp_expert[g] * a.stride : a.shared;
+        r.p0 = g < ng ? s_grp_start[g] : n_ent;
+        r.n_e = g < ng ? s_grp_start[g + 1] - r.p0 : T;
+        r.j = sl - g * spg;
+        return r;
+    };
     v4i reg[kWLoadsA];
-    auto issue = [&](int c) {
-        const gbl_ptr<const v4i> src =
-            gbl_at<v4i>((uintptr_t) (blob + (w_up ? L.up_off : 0) + (uint64_t) (kSliceA * j + c * rows_c + wr0) * gu_row));
+    auto issue = [&](const Slice& si, int c) {
+        const gbl_ptr<const v4i> src = gbl_at<v4i>(
+            (uintptr_t) (si.blob + (w_up ? L.up_off : 0) + (uint64_t) (kSliceA * si.j + c * rows_c + wr0) * gu_row));
 #pragma unroll
         for (int i = 0; i < kWLoadsA; ++i)  // unconditional (clamped) loads keep the wait counts exact
             reg[i] = __builtin_nontemporal_load(src + min(lane + 64 * i, np - 1));
     };
     v4i* wslab = (v4i*) smem + wave * (a.slab_a / 16 / kWavesA);
-    issue(0);
+    Slice cur = slice_at(s0);
+    issue(cur, 0);
+    if (tid < n_ent) s_prow[tid] = div_small(s_pos_ent[tid], k, __builtin_amdgcn_rcpf((float) k));  // position ->
+    if (tid < T) s_prow[n_ent + tid] = tid;                                                            // its token's row
+    __syncthreads();  // activations, codebooks and positions are in LDS
 
-    if (tid < n_e) s_xrow[tid] = is_shared ? tid : s_pos_ent[p0 + tid] / k;  // entry c's LDS row: its token
-    __syncthreads();  // activations and codebooks are in LDS
-
-    // 3. each chunk: the wave's rows into its LDS slab, then against every entry, tpr lanes per row
+    // 4. each chunk: the wave's rows into its LDS slab, then against every entry of the slice's group, tpr lanes per
+    //    row; a finished slice's h = silu(gate) * up and its Q8_1 block for each entry
     const int tpr = 64 / rpw;
     const int lr = lane / tpr, l = lane % tpr;
     const uint8_t* row = (const uint8_t*) wslab + (uint64_t) lr * gu_row;
-    for (int c = 0; c < nchunks; ++c) {
+    for (int sl = s0; sl < s1; ++sl) {
+        const Slice nxt = sl + 1 < s1 ? slice_at(sl + 1) : cur;
+        const int p0 = cur.p0, n_e = cur.n_e;
+        for (int c = 0; c < nchunks; ++c) {
 #pragma unroll
-        for (int i = 0; i < kWLoadsA; ++i)
-            if (lane + 64 * i < np) wslab[lane + 64 * i] = reg[i];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's LDS writes land before its reads
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        if (c + 1 < nchunks) issue(c + 1);
-        for (int e0 = 0; e0 < n_e; e0 += kNC) {
-            const int n = min(kNC, n_e - e0);
-            float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
-            for (int u = l; u < NU; u += tpr) {
-                Unit w;
-                unit_load<GT>(row, u, w, grid);
+            for (int i = 0; i < kWLoadsA; ++i)
+                if (lane + 64 * i < np) wslab[lane + 64 * i] = reg[i];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's LDS writes land before its reads
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            if (c + 1 < nchunks) issue(cur, c + 1);
+            else if (sl + 1 < s1) issue(nxt, 0);
+            for (int e0 = 0; e0 < n_e; e0 += kNC) {
+                const int n = min(kNC, n_e - e0);
+                float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
+                for (int u = l; u < NU; u += tpr) {
+                    Unit w;
+                    unit_load<GT>(row, u, w, grid);
 #pragma unroll
-                for (int cc = 0; cc < kNC; ++cc) {
-                    if (cc < n) {
-                        Act xa;
-                        const int xr = s_xrow[e0 + cc];
-                        act_planes(s_xq + xr * N + 32 * u, s_xd + xr * NU + u, xa);
-                        int S, M;
-                        acc[cc] += unit_dot<GT>(w, xa, S, M);
+                    for (int cc = 0; cc < kNC; ++cc) {
+                        if (cc < n) {
+                            Act xa;
+                            const int xr = s_prow[p0 + e0 + cc];
+                            act_planes(s_xq + xr * N + 32 * u, s_xd + xr * NU + u, xa);
+                            int S, M;
+                            acc[cc] += unit_dot<GT>(w, xa, S, M);
+                        }
                     }
                 }
+                switch (tpr) {  // the tpr lanes of a row are consecutive and tpr divides 64
+                    case 16: sum_acc<16>(acc, T); break;
+                    case 32: sum_acc<32>(acc, T); break;
+                    default: sum_acc<64>(acc, T); break;
+                }
+                if (l == 0) {
+                    const int col = (w_up ? kSliceA : 0) + c * rows_c + wr0 + lr;
+                    for (int cc = 0; cc < n; ++cc) s_gu[e0 + cc][col] = acc[cc];
+                }
             }
-            switch (tpr) {  // the tpr lanes of a row are consecutive and tpr divides 64
-                case 16: sum_acc<16>(acc); break;
-                case 32: sum_acc<32>(acc); break;
-                default: sum_acc<64>(acc); break;
-            }
-            if (l == 0) {
-                const int col = (w_up ? kSliceA : 0) + c * rows_c + wr0 + lr;
-                for (int cc = 0; cc < n; ++cc) s_gu[e0 + cc][col] = acc[cc];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's reads are done before the next chunk
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        }
+        __syncthreads();
+        {  // 32-lane group e takes entry e (all lanes take part)
+            const int e = min(tid >> 5, kMaxTok - 1), i = tid & 31;
+            const float gt = s_gu[e][i];
+            const float h = (gt / (1.0f + expf(-gt))) * s_gu[e][kSliceA + i];
+            const float amax = lanes_reduce<32>(fabsf(h), OpMax());
+            const float dd = q8_1_finite(amax / 127.0f);
+            if ((tid >> 5) < n_e) {
+                const int64_t p = p0 + e;
+                a.hc[p * FF + kSliceA * cur.j + i] = (int8_t) q8_1_code(h, amax, dd);
+                if (i == 0) a.hd[p * (FF / 32) + cur.j] = h2f(f2h(dd));
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's reads are done before the next chunk
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    }
-    __syncthreads();
-
-    // h = silu(gate) * up and its Q8_1 block for each entry: 32-lane group c takes entry c (all lanes take part)
-    const int c = min(tid >> 5, kMaxTok - 1), i = tid & 31;
-    const float g = s_gu[c][i];
-    const float h = (g / (1.0f + expf(-g))) * s_gu[c][kSliceA + i];
-    const float amax = lanes_reduce<32>(fabsf(h), OpMax());
-    const float dd = q8_1_finite(amax / 127.0f);
-    if ((tid >> 5) < n_e) {
-        const int64_t p = p0 + c;
-        a.hc[p * FF + kSliceA * j + i] = (int8_t) q8_1_code(h, amax, dd);
-        if (i == 0) a.hd[p * (FF / 32) + j] = h2f(f2h(dd));
+        if (sl + 1 < s1) __syncthreads();  // s_gu is free for the next slice
+        cur = nxt;
     }
 }
 
@@ -437,11 +474,11 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
                     }
                 }
                 switch (tpr) {
-                    case 4: sum_acc<4>(acc); break;
-                    case 8: sum_acc<8>(acc); break;
-                    case 16: sum_acc<16>(acc); break;
-                    case 32: sum_acc<32>(acc); break;
-                    default: sum_acc<64>(acc); break;
+                    case 4: sum_acc<4>(acc, T); break;
+                    case 8: sum_acc<8>(acc, T); break;
+                    case 16: sum_acc<16>(acc, T); break;
+                    case 32: sum_acc<32>(acc, T); break;
+                    default: sum_acc<64>(acc, T); break;
                 }
                 if (l == 0)
                     for (int cc = 0; cc < n; ++cc) s_part[e0 + cc][rr] = acc[cc];
@@ -571,13 +608,13 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
     a.n_expert = n_expert;
     a.k = k;
     a.n_tok = n_tok;
-    a.cap_groups = std::min(n_tok * k, n_expert);
     a.logits = logits;
     a.x = x;
     a.shared = (const uint8_t*) shared;
     a.sgate = sgate;
     a.sg_stride = sg_stride;
     a.rows_c = rows_c;
+    a.chunks_a = kSliceA / rows_c;
     a.slab_a = slab_a;
     a.slab_b = slab_b;
     a.y = y;
@@ -591,8 +628,9 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
     int rc = with_type(L.gu_type, [&](auto T) {
         auto kern = layer_gu_kernel<decltype(T)::value>;
         const size_t lds = (size_t) slab_a + fixed_a;
-        const dim3 grid((unsigned) (L.n_ff / kSliceA), (unsigned) (a.cap_groups + (shared ? 1 : 0)));
-        kern<<<grid, kThreadsA, lds, s>>>(a);
+        // as many blocks as the routing could give slices, at most one per CU
+        const int most = (std::min(n_tok * k, n_expert) + (shared ? 1 : 0)) * (int) (L.n_ff / kSliceA);
+        kern<<<std::min(kBlocksA, most), kThreadsA, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/gate-up");
     });
     if (rc != TSX_OK) return rc;
