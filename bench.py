@@ -175,7 +175,21 @@ def main() -> int:
     reps = max(3, min(20, args.steps // 5))
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    if prefill:
+    if prefill and mls[0].fused_prefill:
+        # the grouped gate/up product with SwiGLU and the Q8_1 of h fused in, every layer, on the current stream
+        def dom():
+            for ml in mls:
+                W = ml.W
+                ops.mmq_gate_up_swiglu(W.blobs, L.gu_type, FF, N, W.stride, W.n_expert, ml.txq, T, ml.sort[2],
+                                       ml.sort[0], ml.n_ent, hq=ml.mhq)
+        # the distinct experts' gate/up rows, each token's Q8_1 row once, h's Q8_1 rows out
+        gu_bytes = 2 * FF * L.gu_row
+        dom_bytes = float(np.mean([n * gu_bytes + T * (N + N // 32 * 8) + ml.n_ent * (FF + FF // 32 * 8)
+                                   for n, ml in zip(distinct_per_layer, mls)]))
+        dom_ops = 2.0 * T * k * 2 * FF * N
+        kernel = ("mmq_f16_kernel<fused> (grouped gate/up product with SwiGLU and the Q8_1 of h, "
+                  "v_mfma_f32_16x16x32_f16 on exact integer codes) per layer")
+    elif prefill:
         # the grouped gate/up product (f16 MFMA on exact integer codes) of every layer, on the current stream
         def dom():
             for ml in mls:

@@ -174,6 +174,17 @@ TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream);
 /* h[r][k] = silu(g) * u of GU rows [2*n_ff wide]: interleaved (gate 2k, up 2k+1) or split (gate k, up n_ff + k).
  * Replaces strata::prefill::mmq::swiglu (include/strata/prefill/moe_mmq.hpp:112; src/prefill/moe_mmq.cu:123-131). */
 TSX_API int tsx_moe_mmq_swiglu(const float* gu, float* h, int64_t rows, int64_t n_ff, int interleaved, void* stream);
+/* The gate/up product of the prompt path with SwiGLU and the Q8_1 quantization of h fused in: for each expert's
+ * sorted rows [bounds[e], bounds[e+1]) (rows of xq taken through xids, or the sorted rows themselves when xids is
+ * NULL), h = silu(x . gate) * (x . up) quantized into hq (tsx_moe_mmq_q8_bytes(n_rows, n_ff) bytes, row r = sorted
+ * row r), the codes tsx_moe_mmq_quantize writes for the same h.  Gate rows are rows [0, n_ff) of each expert's
+ * matrix, up rows [n_ff, 2 n_ff).  No single reference function: it stands in for the sequence mmq::quantize of the
+ * gathered rows, Context::run of the gate/up product, mmq::swiglu and mmq::quantize of h
+ * (src/qwen35/q36_engine.cu:2855-2872; src/prefill/moe_mmq.cu:123-131, 309-384), the x rows quantized once per
+ * token instead of once per routed row. */
+TSX_API int tsx_moe_mmq_gate_up_swiglu(const void* w, int type, int64_t n_ff, int64_t n_embd, uint64_t expert_bytes,
+                                       int n_exp, const void* xq, int64_t x_rows, const int32_t* xids,
+                                       const int32_t* bounds, int64_t n_rows, void* hq, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ checks and data */
 /* The integer contract: sums[(r*ncols + c)*nsub + u] = sum over sub-block u (32 values) of w_int * a_int, and

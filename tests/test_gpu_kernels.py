@@ -273,3 +273,65 @@ def test_mmq_run_skewed_groups(t, w_cols, w_rows):
             exp[ids[r0:r1]] = O.mmvq_q8_1(t, W[i], w_cols, w_rows, xb[r0:r1], r1 - r0)
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * np.abs(exp).max())
+
+
+def _planes(buf, rows: int, cols: int):
+    """The Q8_1 planes of tsx_moe_mmq_q8_bytes: codes, block scales and code sums of the first `rows` rows."""
+    b = host(buf)
+    rp = (rows + 63) // 64 * 64 + 64
+    a256 = lambda v: (v + 255) // 256 * 256
+    q = b[: rp * cols].view(np.int8).reshape(rp, cols)[:rows]
+    o = a256(rp * cols)
+    d = b[o: o + rp * (cols // 32) * 4].view(np.float32).reshape(rp, cols // 32)[:rows]
+    o += a256(rp * (cols // 32) * 4)
+    m = b[o: o + rp * (cols // 32) * 4].view(np.int32).reshape(rp, cols // 32)[:rows]
+    return q, d, m
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("N,FF", [(512, 128), (2048, 384)])
+@pytest.mark.parametrize("gather", [False, True])
+def test_mmq_gate_up_swiglu_matches_the_call_sequence(t, N, FF, gather):
+    """The fused gate/up + SwiGLU + Q8_1 launch against the reference's sequence on the GPU (gather-quantize, gate/up
+    product, swiglu, quantize of h): the same planes byte for byte, over experts with 0, 70, 1, 130 and 17 rows whose
+    activation rows are token rows taken through a map (gather) or the sorted rows themselves; and h against the
+    oracle's SwiGLU of its own dot products, to the Q8_1 rounding."""
+    rng = np.random.default_rng(t * 11 + N + FF + gather)
+    counts = [0, 70, 1, 130, 17]
+    n, total = len(counts), sum(counts)
+    bounds = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    W = [ops.quantize_weights(t, rng.normal(0, 0.05, (2 * FF, N)).astype(np.float32)) for _ in range(n)]
+    rb = W[0].shape[1]
+    eb = (2 * FF * rb + 255) // 256 * 256
+    blob = np.zeros(n * eb, np.uint8)
+    for i, m in enumerate(W):
+        blob[i * eb: i * eb + m.size] = m.ravel()
+    n_tok = 150 if gather else total
+    x = rng.normal(0, 1, (n_tok, N)).astype(np.float32)
+    x[:, rng.choice(N, N // 50, replace=False)] *= 20.0  # outlier channels
+    xids = rng.integers(0, n_tok, total).astype(np.int32) if gather else np.arange(total, dtype=np.int32)
+    blob_d, bounds_d = dev(blob), dev(bounds)
+    # the reference's sequence
+    xq_rows = ops.mmq_quantize(dev(x), dev(xids), t, N, N, total)
+    gu = torch.empty((total, 2 * FF), device="cuda")
+    ops.mmq_run(blob_d, t, 2 * FF, N, eb, n, xq_rows, bounds_d, None, total, gu, 2 * FF)
+    h = ops.mmq_swiglu(gu, total, FF)
+    ref = ops.mmq_quantize(h, None, t, FF, FF, total)
+    # fused
+    xq_tok = ops.mmq_quantize(dev(x), None, t, N, N, n_tok)
+    got = ops.mmq_gate_up_swiglu(blob_d, t, FF, N, eb, n, xq_tok, n_tok, dev(xids) if gather else None, bounds_d,
+                                 total)
+    gq, gd, gm = _planes(got, total, FF)
+    rq, rd, rm = _planes(ref, total, FF)
+    assert (gq == rq).all() and (gd.view(np.int32) == rd.view(np.int32)).all() and (gm == rm).all()
+    # h against the oracle: SwiGLU of the oracle's gate / up dots on the same Q8_1 codes
+    xb = O.quantize_q8_1(x[xids])
+    hx = np.zeros((total, FF), np.float64)
+    for i in range(n):
+        r0, r1 = bounds[i], bounds[i + 1]
+        if r1 > r0:
+            o = O.mmvq_q8_1(t, W[i], N, 2 * FF, xb[r0:r1], r1 - r0)
+            g, u = o[:, :FF], o[:, FF:]
+            hx[r0:r1] = g / (1.0 + np.exp(-g)) * u
+    hd = gq.reshape(total, FF // 32, 32).astype(np.float64) * gd[:, :, None]
+    assert rel_l2(hd.reshape(total, FF), hx) < 2e-2

@@ -281,12 +281,16 @@ __device__ __forceinline__ int block_scan(int v, int* s_wave, int& total) {
     return off + inc - v;
 }
 
-template <int T, int NW>
+// FUSE: the gate/up product with SwiGLU and the Q8_1 of h fused in (NW = 8).  Block bx takes gate rows
+// [128 bx, 128 bx + 128) in waves 0-3 and the matching up rows (n_ff further) in waves 4-7; the activation rows are
+// xids[sorted row] of P (sorted row r itself when xids is null); h leaves as Q8_1 planes H, one row per sorted row.
+template <int T, int NW, bool FUSE = false>
 __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restrict__ w, uint64_t expert_bytes,
                                                           uint64_t row_bytes, int w_cols, int n_exp, MmqPlanes P,
                                                           const int32_t* __restrict__ bounds,
                                                           const int32_t* __restrict__ ids, float* __restrict__ dst,
-                                                          int64_t ld_dst) {
+                                                          int64_t ld_dst, const int32_t* __restrict__ xids = nullptr,
+                                                          MmqPlanes H = MmqPlanes{}, int n_ff = 0) {
     constexpr int NT = 64 * NW, BM = 32 * NW, NB = f16_buffers<T, NW>();
     constexpr int CB = chunk_bytes<T>(), RS = raw_stride<T>(), PR = RS / 16, RW = (32 * PR + 63) / 64;
     constexpr int BP = kBN * 16 / NT, DP = kBN * 8 / NT, EPT = kMaxExpertsMmq / NT;
@@ -332,8 +336,21 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     const int row0 = bounds[x] + (by - s_tile0) * kBN;
     const int nrows = min(kBN, bounds[x + 1] - row0);
     const int ntt = (nrows + 15) >> 4;  // 16-token MFMA tiles with rows in them
-    const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) (bx * BM + 32 * wave) * row_bytes;
+    const int wrow = FUSE ? (wave < NW / 2 ? 0 : n_ff) + (BM / 2) * bx + 32 * (wave % (NW / 2)) : bx * BM + 32 * wave;
+    const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) wrow * row_bytes;
     const int nu = w_cols / 32, nchunks = w_cols / kChunk;
+    // the activation rows this thread loads (the same every chunk): rows past the tile's last take its last row
+    int64_t arow_b[BP], arow_d[DP];
+#pragma unroll
+    for (int h = 0; h < BP; ++h) {
+        const int rr = (tid + NT * h) >> 4;
+        arow_b[h] = xids ? (int64_t) xids[row0 + min(rr, nrows - 1)] : (int64_t) (row0 + rr);
+    }
+#pragma unroll
+    for (int h = 0; h < DP; ++h) {
+        const int rr = (tid + NT * h) >> 3;
+        arow_d[h] = xids ? (int64_t) xids[row0 + min(rr, nrows - 1)] : (int64_t) (row0 + rr);
+    }
 
     // chunk c in flight: this wave's raw weight pieces, the block's share of activation codes and scales
     v4i rw[RW], av[BP];
@@ -349,13 +366,13 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
         }
 #pragma unroll
         for (int h = 0; h < BP; ++h) {
-            const int pi = tid + NT * h, rr = pi >> 4, q = pi & 15;
-            av[h] = *(const v4i*) (P.q + (int64_t) (row0 + rr) * P.cols + kChunk * c + 16 * q);
+            const int pi = tid + NT * h, q = pi & 15;
+            av[h] = *(const v4i*) (P.q + arow_b[h] * P.cols + kChunk * c + 16 * q);
         }
 #pragma unroll
         for (int h = 0; h < DP; ++h) {
-            const int e = tid + NT * h, rr = e >> 3, u = e & 7;
-            const int64_t o = (int64_t) (row0 + rr) * nu + 8 * c + u;
+            const int e = tid + NT * h, u = e & 7;
+            const int64_t o = arow_d[h] * nu + 8 * c + u;
             ad[h] = P.d[o];
             if constexpr (Q4K) am[h] = P.m[o];
         }
@@ -580,17 +597,78 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             }
         }
 
-        // out: weight row 16 t + 4 g + i of the wave, token 16 tj + lr
+        if constexpr (FUSE) {
+#pragma clang fp contract(off)
+            // the block's gate (columns 0-127) and up (128-255) outputs through LDS, in runs of TOK tokens: the
+            // activation tiles' LDS once every wave is past its last chunk
+            constexpr int OS = 2 * (BM / 2) + 1;  // floats per token: odd, so 16 tokens' writes hit distinct banks
+            constexpr int TOK = NB * kBN * kBStride * 2 >= kBN * OS * 4 ? kBN : kBN / 2;
+            float* so = (float*) &tB[0][0];
+            __syncthreads();
+            for (int t0 = 0; t0 < 16 * NTT; t0 += TOK) {
 #pragma unroll
-        for (int tj = 0; tj < NTT; ++tj) {
-            const int tok = 16 * tj + lr;
-            if (tok < nrows) {
-                const int64_t drow = ids ? ids[row0 + tok] : row0 + tok;
-                float* o = dst + drow * ld_dst + (int64_t) bx * BM + 32 * wave + 4 * g;
+                for (int tj = 0; tj < NTT; ++tj) {
+                    const int tok = 16 * tj + lr - t0;
+                    if (tok >= 0 && tok < TOK)
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+                        for (int t = 0; t < 2; ++t)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) o[16 * t + i] = acc[t][tj][i];
+                            for (int i = 0; i < 4; ++i) so[tok * OS + 32 * wave + 16 * t + 4 * g + i] = acc[t][tj][i];
+                }
+                __syncthreads();
+                // h = silu(gate) * up (the product rounded on its own) and its Q8_1 blocks: 8 lanes per 32 values,
+                // 4 each, every lane taking part in the reductions
+                const int ntok = min(TOK, 16 * NTT - t0);  // a multiple of 16: whole rounds of the block
+                for (int q0 = 0; q0 < ntok * (BM / 8); q0 += NT) {
+                    const int q = q0 + tid, tok = q / (BM / 8), f4 = q % (BM / 8);
+                    const float* gp = so + tok * OS + 4 * f4;
+                    float hv[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const float gt = gp[k];
+                        hv[k] = (gt / (1.0f + expf(-gt))) * gp[BM / 2 + k];
+                    }
+                    float amax = fmaxf(fmaxf(fabsf(hv[0]), fabsf(hv[1])), fmaxf(fabsf(hv[2]), fabsf(hv[3])));
+                    amax = lanes_reduce<8>(amax, OpMax());
+                    const float d = q8_1_finite(amax / 127.0f);
+                    int qv[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        int v = 0;
+                        if (amax != 0.0f) {
+                            const float r = roundf(hv[k] / d);
+                            v = (int) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
+                        }
+                        qv[k] = v;
+                    }
+                    const float qs = lanes_reduce<8>((float) (qv[0] + qv[1] + qv[2] + qv[3]), OpAddF());
+                    if (t0 + tok < nrows) {
+                        const int64_t hr = row0 + t0 + tok, col = (int64_t) (BM / 2) * bx + 4 * f4;
+                        *(uint32_t*) (H.q + hr * H.cols + col) = ((uint32_t) qv[0] & 0xFFu) |
+                                                                 ((uint32_t) qv[1] & 0xFFu) << 8 |
+                                                                 ((uint32_t) qv[2] & 0xFFu) << 16 |
+                                                                 ((uint32_t) qv[3] & 0xFFu) << 24;
+                        if ((f4 & 7) == 0) {
+                            H.d[hr * (H.cols / 32) + col / 32] = h2f(f2h(q8_1_finite(d)));
+                            H.m[hr * (H.cols / 32) + col / 32] = (int32_t) qs;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        } else {
+            // out: weight row 16 t + 4 g + i of the wave, token 16 tj + lr
+#pragma unroll
+            for (int tj = 0; tj < NTT; ++tj) {
+                const int tok = 16 * tj + lr;
+                if (tok < nrows) {
+                    const int64_t drow = ids ? ids[row0 + tok] : row0 + tok;
+                    float* o = dst + drow * ld_dst + (int64_t) bx * BM + 32 * wave + 4 * g;
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) o[16 * t + i] = acc[t][tj][i];
+                }
             }
         }
     };
@@ -716,6 +794,34 @@ TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
                 p->ld_dst);
             return launch_status("tsx_moe_mmq_run");
         });
+    });
+}
+
+TSX_API int tsx_moe_mmq_gate_up_swiglu(const void* w, int type, int64_t n_ff, int64_t n_embd, uint64_t expert_bytes,
+                                       int n_exp, const void* xq, int64_t x_rows, const int32_t* xids,
+                                       const int32_t* bounds, int64_t n_rows, void* hq, void* stream) {
+    const size_t rb = tsx_row_bytes(type, n_embd);
+    if (!tsx_weight_type_ok(type) || rb == 0 || n_embd % kChunk != 0 || n_ff <= 0 || n_ff % 128 != 0 ||
+        n_exp > kMaxExpertsMmq) {
+        set_error("tsx_moe_mmq_gate_up_swiglu: type %d, %lld x %lld, %d experts not supported (n_embd a multiple of "
+                  "256, n_ff of 128, at most %d experts)",
+                  type, (long long) n_embd, (long long) n_ff, n_exp, kMaxExpertsMmq);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    TSX_REQUIRE(w && xq && bounds && hq && n_exp >= 0 && x_rows >= 0 && n_rows >= 0 && aligned(w, 16) &&
+                    expert_bytes % 16 == 0 && expert_bytes >= rb * (uint64_t) (2 * n_ff) && aligned(xq, 256) &&
+                    aligned(hq, 256),
+                "tsx_moe_mmq_gate_up_swiglu: w, xq, bounds, hq (xq and hq 256-byte aligned, w and expert_bytes "
+                "16-byte), expert_bytes >= the gate and up rows");
+    if (n_exp == 0 || n_rows == 0) return TSX_OK;
+    const MmqPlanes P = planes((void*) xq, x_rows, n_embd), H = planes(hq, n_rows, n_ff);
+    const hipStream_t s = (hipStream_t) stream;
+    const int64_t max_tiles = (n_rows + kBN - 1) / kBN + n_exp;
+    return with_type(type, [&](auto T) {
+        const dim3 grid((unsigned) (n_ff / 128), (unsigned) max_tiles);
+        mmq_f16_kernel<decltype(T)::value, 8, true><<<grid, 512, 0, s>>>(
+            (const uint8_t*) w, expert_bytes, rb, (int) n_embd, n_exp, P, bounds, nullptr, nullptr, 0, xids, H, (int) n_ff);
+        return launch_status("tsx_moe_mmq_gate_up_swiglu");
     });
 }
 

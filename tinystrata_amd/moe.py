@@ -113,16 +113,24 @@ class MoELayer:
             self.sort = (torch.empty(W.n_expert + 1, dtype=i32, device=dev), torch.empty(n_ent, dtype=i32, device=dev),
                          torch.empty(n_ent, dtype=i32, device=dev), torch.empty(n_ent, dtype=i32, device=dev),
                          torch.empty(1, dtype=i32, device=dev))
-            self.mxq = torch.empty(ops.mmq_q8_bytes(n_ent, self.N), dtype=torch.uint8, device=dev)
-            self.gu = torch.empty((n_ent, 2 * self.FF), dtype=f32, device=dev)
-            self.h = torch.empty((n_ent, self.FF), dtype=f32, device=dev)
+            # gate/up with SwiGLU and the Q8_1 of h in one launch, reading each token's activations quantized once,
+            # where the shape allows; else the reference's call sequence
+            self.fused_prefill = (fused and self.N % 256 == 0 and self.FF % 128 == 0 and W.n_expert <= 512 and
+                                  int(L.up_off) == self.FF * int(L.gu_row))
             self.mhq = torch.empty(ops.mmq_q8_bytes(n_ent, self.FF), dtype=torch.uint8, device=dev)
+            if self.fused_prefill:
+                self.txq = torch.empty(ops.mmq_q8_bytes(n_tok, self.N), dtype=torch.uint8, device=dev)
+            else:
+                self.mxq = torch.empty(ops.mmq_q8_bytes(n_ent, self.N), dtype=torch.uint8, device=dev)
+                self.gu = torch.empty((n_ent, 2 * self.FF), dtype=f32, device=dev)
+                self.h = torch.empty((n_ent, self.FF), dtype=f32, device=dev)
             if W.shared is not None:
                 self.sh_bounds = torch.tensor([0, n_tok], dtype=i32, device=dev)
-                self.sxq = torch.empty(ops.mmq_q8_bytes(n_tok, self.N), dtype=torch.uint8, device=dev)
-                self.sgu = torch.empty((n_tok, 2 * self.FF), dtype=f32, device=dev)
-                self.sh_h = torch.empty((n_tok, self.FF), dtype=f32, device=dev)
                 self.shq = torch.empty(ops.mmq_q8_bytes(n_tok, self.FF), dtype=torch.uint8, device=dev)
+                if not self.fused_prefill:
+                    self.sxq = torch.empty(ops.mmq_q8_bytes(n_tok, self.N), dtype=torch.uint8, device=dev)
+                    self.sgu = torch.empty((n_tok, 2 * self.FF), dtype=f32, device=dev)
+                    self.sh_h = torch.empty((n_tok, self.FF), dtype=f32, device=dev)
 
     def __call__(self, x: torch.Tensor, logits: torch.Tensor, sgate: torch.Tensor | None, y: torch.Tensor) -> None:
         """y += MoE(x): x, y [n_tok, N] float32; logits [n_tok, E]; sgate [n_tok] (shared expert gate logit)."""
@@ -151,6 +159,9 @@ class MoELayer:
         ops.native_router_topk(logits, k, self.ids, self.wts)
         bounds, ed, et, rinv, mr = ops.route_sort(self.ids, k, W.n_expert, bufs=self.sort)
         n_ent = self.n_ent
+        if self.fused_prefill:
+            self._prefill_fused(x, sgate, y, bounds, et, rinv)
+            return
         ops.mmq_quantize(x, et, L.gu_type, N, N, n_ent, xq=self.mxq)
         ops.mmq_run(W.blobs, L.gu_type, 2 * FF, N, W.stride, W.n_expert, self.mxq, bounds, None, n_ent, self.gu, 2 * FF)
         ops.mmq_swiglu(self.gu, n_ent, FF, False, h=self.h)
@@ -164,5 +175,18 @@ class MoELayer:
             ops.mmq_run(sh, L.gu_type, 2 * FF, N, W.stride, 1, self.sxq, self.sh_bounds, None, T, self.sgu, 2 * FF)
             ops.mmq_swiglu(self.sgu, T, FF, False, h=self.sh_h)
             ops.mmq_quantize(self.sh_h, None, L.d_type, FF, FF, T, xq=self.shq)
+            ops.mmq_run(sh[L.down_off:], L.d_type, N, FF, W.stride, 1, self.shq, self.sh_bounds, None, T, self.sh, N)
+        ops.moe_combine(y, self.parts, self.wts, k, prow=rinv, shared=self.sh, sgate=sgate)
+
+    def _prefill_fused(self, x, sgate, y, bounds, et, rinv):
+        W, L, k, N, FF, T = self.W, self.W.L, self.k, self.N, self.FF, self.n_tok
+        ops.mmq_quantize(x, None, L.gu_type, N, N, T, xq=self.txq)  # every token once; routed rows read it via et
+        ops.mmq_gate_up_swiglu(W.blobs, L.gu_type, FF, N, W.stride, W.n_expert, self.txq, T, et, bounds, self.n_ent,
+                               hq=self.mhq)
+        ops.mmq_run(W.blobs[L.down_off:], L.d_type, N, FF, W.stride, W.n_expert, self.mhq, bounds, None, self.n_ent,
+                    self.parts, N)
+        if W.shared is not None:
+            sh = W.shared
+            ops.mmq_gate_up_swiglu(sh, L.gu_type, FF, N, W.stride, 1, self.txq, T, None, self.sh_bounds, T, hq=self.shq)
             ops.mmq_run(sh[L.down_off:], L.d_type, N, FF, W.stride, 1, self.shq, self.sh_bounds, None, T, self.sh, N)
         ops.moe_combine(y, self.parts, self.wts, k, prow=rinv, shared=self.sh, sgate=sgate)

@@ -181,6 +181,17 @@ def mmq_swiglu(gu, rows: int, n_ff: int, interleaved: bool = False, h=None, stre
     return h
 
 
+def mmq_gate_up_swiglu(w, ggml_type: int, n_ff: int, n_embd: int, expert_bytes: int, n: int, xq, x_rows: int, xids,
+                       bounds, n_rows: int, hq=None, stream=None) -> torch.Tensor:
+    """h = silu(x . gate) * (x . up) of every expert's sorted rows (x rows through xids), quantized into Q8_1 planes
+    of n_rows rows and n_ff columns (the layout mmq_quantize writes)."""
+    if hq is None:
+        hq = torch.empty(mmq_q8_bytes(n_rows, n_ff), dtype=torch.uint8, device=w.device)
+    check(lib().tsx_moe_mmq_gate_up_swiglu(_p(w), ggml_type, n_ff, n_embd, expert_bytes, n, _p(xq), x_rows, _p(xids),
+                                            _p(bounds), n_rows, _p(hq), _stream(stream)), "mmq_gate_up_swiglu")
+    return hq
+
+
 # ------------------------------------------------------------------ checks and data
 def subblock_sums(ggml_type: int, w, n_in: int, n_rows: int, x_q8_1, ncols: int, stream=None):
     nsub = n_in // 32
