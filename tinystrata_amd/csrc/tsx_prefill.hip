@@ -489,12 +489,9 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             }
 #pragma unroll 1
             for (int up = 0; up < 8; up += 2) {
-              float2 dx2[NTT], dm2[NTT];
+              float2 dx2[NTT];
 #pragma unroll
-              for (int tj = 0; tj < NTT; ++tj) {
-                  dx2[tj] = *(const float2*) &s_dx[buf][16 * tj + lr][up];
-                  if constexpr (Q4K) dm2[tj] = *(const float2*) &s_dm[buf][16 * tj + lr][up];
-              }
+              for (int tj = 0; tj < NTT; ++tj) dx2[tj] = *(const float2*) &s_dx[buf][16 * tj + lr][up];
 #pragma unroll
               for (int k = 0; k < 2; ++k) {
                 const int u = up + k;
@@ -542,9 +539,9 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     }
                     A[t] = v4i{(int) f[0], (int) f[1], (int) f[2], (int) f[3]};
                 }
-                // per-output-row unit factors (Q4_K min, Q8_0 scale): rows 16 t + 4 g + i
+                // per-output-row unit factors (Q8_0 scale): rows 16 t + 4 g + i
                 float4 uf[2];
-                if constexpr (Q4K || Q80) {
+                if constexpr (Q80) {
 #pragma unroll
                     for (int t = 0; t < 2; ++t) uf[t] = *(const float4*) &s_uf[wave][u][16 * t + 4 * g];
                 }
@@ -553,8 +550,6 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     const int tok = 16 * tj + lr;
                     const v4i Bf = *(const v4i*) (B + tok * kBStride + 32 * u + 8 * g);
                     const float dx = k == 0 ? dx2[tj].x : dx2[tj].y;
-                    float dm = 0.f;
-                    if constexpr (Q4K) dm = k == 0 ? dm2[tj].x : dm2[tj].y;
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
                         const v4f z = {0.f, 0.f, 0.f, 0.f};
@@ -563,16 +558,34 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                         const float ufa[4] = {uf[t].x, uf[t].y, uf[t].z, uf[t].w};
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            if constexpr (Q80) {
-                                acc[t][tj][i] += (ufa[i] * dx) * D[i];
-                            } else {
-                                tacc[t][tj][i] += dx * D[i];
-                                if constexpr (Q4K) acc[t][tj][i] -= ufa[i] * dm;
-                            }
+                            if constexpr (Q80) acc[t][tj][i] += (ufa[i] * dx) * D[i];
+                            else tacc[t][tj][i] += dx * D[i];
                         }
                     }
                 }
               }
+            }
+            if constexpr (Q4K) {
+                // the chunk's min term, sum over units u of (dmin m)[row][u] * (dx s)[token][u]: a [rows x 8] by
+                // [8 x tokens] product on the fp32 matrix cores (two K = 4 steps), rows 16 t + lr by units 4 h + g
+                // in A, units by tokens 16 tj + lr in B, accumulated into the outputs
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    float am[2];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) am[t] = -s_uf[wave][4 * h + g][16 * t + lr];
+#pragma unroll
+                    for (int tj = 0; tj < NTT; ++tj) {
+                        const float bm = s_dm[buf][16 * tj + lr][4 * h + g];
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) {
+                            const v4f C = {acc[t][tj][0], acc[t][tj][1], acc[t][tj][2], acc[t][tj][3]};
+                            const v4f D = __builtin_amdgcn_mfma_f32_16x16x4f32(am[t], bm, C, 0, 0, 0);
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) acc[t][tj][i] = D[i];
+                        }
+                    }
+                }
             }
             if constexpr (!Q80) {  // the chunk's row scale
 #pragma unroll
