@@ -313,6 +313,20 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
             else if (sl + 1 < s1) issue(nxt, 0);
             for (int e0 = 0; e0 < n_e; e0 += kNC) {
                 const int n = min(kNC, n_e - e0);
+                // the entries' activation rows, looked up once per pass for the block types with a long unit
+                // decode; a Q8_0 unit is a single load and dot, where the four live offsets cost more than the
+                // lookups they save
+                constexpr bool kHoist = GT != TSX_Q8_0;
+                int xo[kNC], xso[kNC];
+#pragma unroll
+                for (int cc = 0; cc < kNC; ++cc) {
+                    xo[cc] = xso[cc] = 0;
+                    if (kHoist && cc < n) {
+                        const int xr = s_prow[p0 + e0 + cc];
+                        xo[cc] = (int) __umul24((unsigned) xr, (unsigned) N);
+                        xso[cc] = (int) __umul24((unsigned) xr, (unsigned) NU);
+                    }
+                }
                 float acc[kNC] = {0.f, 0.f, 0.f, 0.f};
                 for (int u = l; u < NU; u += tpr) {
                     Unit w;
@@ -321,8 +335,12 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
                     for (int cc = 0; cc < kNC; ++cc) {
                         if (cc < n) {
                             Act xa;
-                            const int xr = s_prow[p0 + e0 + cc];
-                            act_planes(s_xq + xr * N + 32 * u, s_xd + xr * NU + u, xa);
+                            if constexpr (kHoist) {
+                                act_planes(s_xq + xo[cc] + 32 * u, s_xd + xso[cc] + u, xa);
+                            } else {
+                                const int xr = s_prow[p0 + e0 + cc];
+                                act_planes(s_xq + xr * N + 32 * u, s_xd + xr * NU + u, xa);
+                            }
                             int S, M;
                             acc[cc] += unit_dot<GT>(w, xa, S, M);
                         }
