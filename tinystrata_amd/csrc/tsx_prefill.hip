@@ -224,6 +224,7 @@ static __constant__ const HalfTables kHalf = make_half_tables();
 template <int T> constexpr int half_grid_words() { return T == TSX_IQ3_XXS ? 512 : T == TSX_IQ3_S ? 1024 : 0; }
 template <int T> constexpr int half_table_words() { return 2 * half_grid_words<T>(); }
 
+constexpr int lds_round(int bytes) { return (bytes + 15) / 16 * 16; }
 template <int T> constexpr int chunk_bytes() { return T == TSX_Q8_0 ? 8 * 34 : Fmt<T>::bytes; }
 // LDS bytes per row of a chunk's raw blocks: the block plus up to 15 bytes of alignment in front of it, rounded to
 // an odd number of 16-byte pieces so that 16 lanes reading the same field of 16 rows hit 16 different bank quads
@@ -256,6 +257,13 @@ __device__ __forceinline__ void nib_to_h(uint32_t w, h2 sc, h2 nsc, uint32_t& lo
     const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u));
     lo = __builtin_bit_cast(uint32_t, a * sc + nsc);
     hi = __builtin_bit_cast(uint32_t, b * sc + nsc);
+}
+// the LDS address of p held in a register the compiler cannot see into, so that constant offsets from it go into
+// the 16-bit offset field of the LDS instructions instead of an add per access
+template <typename T> __device__ __forceinline__ lds_ptr<const T> lds_base(const void* p) {
+    uint32_t a = (uint32_t) (uintptr_t) (lds_ptr<const void>) p;
+    asm volatile("" : "+v"(a));
+    return (lds_ptr<const T>) (uintptr_t) a;
 }
 __device__ __forceinline__ void wave_lds_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
@@ -296,16 +304,33 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     constexpr int BP = kBN * 16 / NT, DP = kBN * 8 / NT, EPT = kMaxExpertsMmq / NT;
     constexpr int TW = half_table_words<T>(), GW = half_grid_words<T>(), TPT = (TW + NT - 1) / NT;
     constexpr bool Q4K = T == TSX_Q4_K, Q80 = T == TSX_Q8_0, IQ3S = T == TSX_IQ3_S;
-    __shared__ __attribute__((aligned(16))) _Float16 tB[NB][kBN * kBStride];
-    __shared__ __attribute__((aligned(16))) float s_dx[NB][kBN][8];
-    __shared__ __attribute__((aligned(16))) float s_dm[Q4K ? NB : 1][Q4K ? kBN : 1][8];
-    __shared__ __attribute__((aligned(16))) uint8_t s_raw[NW][32 * RS];
-    __shared__ __attribute__((aligned(16))) uint32_t s_tab[TW > 0 ? TW : 4];
-    __shared__ __attribute__((aligned(16))) float s_rd[NW][32];                          // row scale per chunk
-    __shared__ __attribute__((aligned(16))) uint32_t s_sc[IQ3S || Q4K ? NW : 1][8][32];  // integer scale as an fp16 pair
-    __shared__ __attribute__((aligned(16))) float s_uf[Q4K || Q80 ? NW : 1][8][32];      // Q4_K: dmin * m; Q8_0: d
-    __shared__ __attribute__((aligned(16))) uint2 s_am[T == TSX_IQ3_XXS ? NW : 1][8][32];  // IQ3_XXS: aux word, m pair
-    __shared__ int s_scan[NW], s_x, s_tile0;
+    // LDS as one array laid out by hand: the codebooks at address 0 and the arrays read per unit next, so that
+    // their addresses fit the 16-bit offsets of the LDS instructions; the raw weight slabs and the activation tiles
+    // last (the compiler would order separate arrays by size, the large ones first)
+    constexpr int XXS = T == TSX_IQ3_XXS;
+    constexpr int O_TAB = 0, O_AM = O_TAB + lds_round((TW > 0 ? TW : 4) * 4);
+    constexpr int O_SC = O_AM + lds_round((XXS ? NW : 1) * 8 * 32 * 8);
+    constexpr int O_UF = O_SC + lds_round((IQ3S || Q4K ? NW : 1) * 8 * 32 * 4);
+    constexpr int O_RD = O_UF + lds_round((Q4K || Q80 ? NW : 1) * 8 * 32 * 4);
+    constexpr int O_DX = O_RD + lds_round(NW * 32 * 4);
+    constexpr int O_DM = O_DX + lds_round(NB * kBN * 8 * 4);
+    constexpr int O_SCAN = O_DM + lds_round((Q4K ? NB * kBN : 1) * 8 * 4);
+    constexpr int O_RAW = O_SCAN + lds_round((NW + 2) * 4);
+    constexpr int O_TB = O_RAW + lds_round(NW * 32 * RS);
+    constexpr int LDS_BYTES = O_TB + NB * kBN * kBStride * 2;
+    __shared__ __attribute__((aligned(16))) uint8_t s_lds[LDS_BYTES];
+    auto& s_tab = *reinterpret_cast<uint32_t(*)[TW > 0 ? TW : 4]>(s_lds + O_TAB);
+    auto& s_am = *reinterpret_cast<uint2(*)[XXS ? NW : 1][8][32]>(s_lds + O_AM);         // IQ3_XXS: aux word, m pair
+    auto& s_sc = *reinterpret_cast<uint32_t(*)[IQ3S || Q4K ? NW : 1][8][32]>(s_lds + O_SC);  // integer scale, fp16 pair
+    auto& s_uf = *reinterpret_cast<float(*)[Q4K || Q80 ? NW : 1][8][32]>(s_lds + O_UF);     // Q4_K: dmin * m; Q8_0: d
+    auto& s_rd = *reinterpret_cast<float(*)[NW][32]>(s_lds + O_RD);                         // row scale per chunk
+    auto& s_dx = *reinterpret_cast<float(*)[NB][kBN][8]>(s_lds + O_DX);
+    auto& s_dm = *reinterpret_cast<float(*)[Q4K ? NB : 1][Q4K ? kBN : 1][8]>(s_lds + O_DM);
+    int* const s_scan = reinterpret_cast<int*>(s_lds + O_SCAN);
+    int& s_x = s_scan[NW];
+    int& s_tile0 = s_scan[NW + 1];
+    auto& s_raw = *reinterpret_cast<uint8_t(*)[NW][32 * RS]>(s_lds + O_RAW);
+    auto& tB = *reinterpret_cast<_Float16(*)[NB][kBN * kBStride]>(s_lds + O_TB);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int bx = blockIdx.x, by = blockIdx.y;
@@ -434,6 +459,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             const int buf = NB == 2 ? (c & 1) : 0;
             const _Float16* B = tB[buf];
             const uint8_t* slab = s_raw[wave];
+            const lds_ptr<const v4i> bq = lds_base<v4i>(B + lr * kBStride + 8 * g);  // this lane's activation pieces
             // the wave's rows: per-row and per-unit factors (lane = row r, units 4 hl .. 4 hl + 3)
             {
                 const int r = lane & 31, hl = lane >> 5;
@@ -487,15 +513,8 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                 const int r = 16 * t + lr;
                 blk[t] = slab + r * RS + (int) (((uint64_t) r * row_bytes + (uint64_t) c * CB) & 15);
             }
-#pragma unroll 1
-            for (int up = 0; up < 8; up += 2) {
-              float2 dx2[NTT];
-#pragma unroll
-              for (int tj = 0; tj < NTT; ++tj) dx2[tj] = *(const float2*) &s_dx[buf][16 * tj + lr][up];
-#pragma unroll
-              for (int k = 0; k < 2; ++k) {
-                const int u = up + k;
-                v4i A[2];
+            // unit u's weight fragments (rows 16 t + lr, values 8 g .. 8 g + 7 of the unit)
+            auto decode = [&](int u, v4i (&A)[2]) {
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     const uint8_t* b = blk[t];
@@ -539,31 +558,58 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     }
                     A[t] = v4i{(int) f[0], (int) f[1], (int) f[2], (int) f[3]};
                 }
+            };
+            // unit u's activation fragments and scales (tokens 16 tj + lr)
+            auto load_b = [&](int u, v4i (&Bf)[NTT], float (&dx)[NTT]) {
+#pragma unroll
+                for (int tj = 0; tj < NTT; ++tj) {
+                    const int tok = 16 * tj + lr;
+                    Bf[tj] = bq[(tj * 16 * kBStride + 32 * u) / 8];
+                    dx[tj] = s_dx[buf][tok][u];
+                }
+            };
+            // software pipeline over the chunk's 8 units: unit u + 1's fragments are read and decoded while unit u's
+            // products run on the matrix cores, and each product is scaled only after the next unit's decode
+            v4i A[2], Bf[NTT];
+            float dx[NTT];
+            decode(0, A);
+            load_b(0, Bf, dx);
+#pragma unroll 1
+            for (int u = 0; u < 8; ++u) {
+                v4f D[2][NTT];
+#pragma unroll
+                for (int tj = 0; tj < NTT; ++tj)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+                        D[t][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, A[t]),
+                                                                         __builtin_bit_cast(v8h, Bf[tj]),
+                                                                         v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                float dxu[NTT];
+#pragma unroll
+                for (int tj = 0; tj < NTT; ++tj) dxu[tj] = dx[tj];
                 // per-output-row unit factors (Q8_0 scale): rows 16 t + 4 g + i
                 float4 uf[2];
                 if constexpr (Q80) {
 #pragma unroll
                     for (int t = 0; t < 2; ++t) uf[t] = *(const float4*) &s_uf[wave][u][16 * t + 4 * g];
                 }
+                if (u + 1 < 8) {
+                    decode(u + 1, A);
+                    load_b(u + 1, Bf, dx);
+                }
 #pragma unroll
-                for (int tj = 0; tj < NTT; ++tj) {
-                    const int tok = 16 * tj + lr;
-                    const v4i Bf = *(const v4i*) (B + tok * kBStride + 32 * u + 8 * g);
-                    const float dx = k == 0 ? dx2[tj].x : dx2[tj].y;
+                for (int tj = 0; tj < NTT; ++tj)
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
-                        const v4f z = {0.f, 0.f, 0.f, 0.f};
-                        const v4f D = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, A[t]),
-                                                                             __builtin_bit_cast(v8h, Bf), z, 0, 0, 0);
                         const float ufa[4] = {uf[t].x, uf[t].y, uf[t].z, uf[t].w};
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            if constexpr (Q80) acc[t][tj][i] += (ufa[i] * dx) * D[i];
-                            else tacc[t][tj][i] += dx * D[i];
+                            if constexpr (Q80) acc[t][tj][i] += (ufa[i] * dxu[tj]) * D[t][tj][i];
+                            else tacc[t][tj][i] += dxu[tj] * D[t][tj][i];
                         }
                     }
-                }
-              }
+#pragma unroll
+                for (int tj = 0; tj < NTT; ++tj) asm volatile("" ::"v"(Bf[tj]), "v"(dx[tj]));  // read in this step
             }
             if constexpr (Q4K) {
                 // the chunk's min term, sum over units u of (dmin m)[row][u] * (dx s)[token][u]: a [rows x 8] by
