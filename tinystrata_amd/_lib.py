@@ -11,7 +11,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libtsx_moe.so"
 
 ABI_VERSION = 1
-TSX_OK, TSX_ERR_UNSUPPORTED, TSX_ERR_ARG = 0, -1, -2
+TSX_OK, TSX_ERR_UNSUPPORTED, TSX_ERR_ARG, TSX_ERR_FORMAT, TSX_ERR_NOT_FOUND = 0, -1, -2, -3, -4
 
 # type ids (ggml's)
 Q8_0, Q8_1, Q4_K, Q8_K, IQ3_XXS, IQ3_S = 8, 9, 12, 15, 18, 21
@@ -53,6 +53,34 @@ class MmqProduct(C.Structure):
     ]
 
 
+class GgufTensor(C.Structure):
+    """tsx_gguf_tensor: one entry of a GGUF tensor directory (reference TensorInfo)."""
+
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("type", C.c_int32),
+        ("n_dims", C.c_int32),
+        ("ne", C.c_int64 * 4),
+        ("offset", C.c_uint64),
+        ("bytes", C.c_uint64),
+        ("data", C.c_void_p),
+        ("shard", C.c_int32),
+    ]
+
+
+class GgufExperts(C.Structure):
+    """tsx_gguf_experts: one layer's routed (or shared) experts inside the mapped model."""
+
+    _fields_ = [
+        ("L", ExpertLayout),
+        ("stride", C.c_uint64),
+        ("n_expert", C.c_int64),
+        ("gate", C.c_void_p),
+        ("up", C.c_void_p),
+        ("down", C.c_void_p),
+    ]
+
+
 P, I32, I64, U64, SZ = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_size_t
 
 # name -> (restype, argtypes); the list is the whole C ABI, checked against include/tsx_moe.h by the tests
@@ -84,6 +112,28 @@ SIGNATURES = {
     "tsx_moe_quantize_weights": (I32, [I32, P, I64, I64, P]),
 }
 
+# the GGUF reader of include/tsx_gguf.h
+GGUF_SIGNATURES = {
+    "tsx_gguf_block_geometry": (I32, [I32, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "tsx_gguf_split_paths": (I32, [C.c_char_p, P, SZ, C.POINTER(C.c_int), C.POINTER(C.c_size_t)]),
+    "tsx_gguf_open": (I32, [C.POINTER(C.c_char_p), I32, C.POINTER(P)]),
+    "tsx_gguf_open_model": (I32, [C.c_char_p, C.POINTER(P)]),
+    "tsx_gguf_close": (None, [P]),
+    "tsx_gguf_shard_count": (I32, [P]),
+    "tsx_gguf_shard_info": (I32, [P, I32, C.POINTER(C.c_uint32), C.POINTER(U64), C.POINTER(U64), C.POINTER(U64)]),
+    "tsx_gguf_tensor_count": (I64, [P]),
+    "tsx_gguf_tensor_at": (I32, [P, I64, C.POINTER(GgufTensor)]),
+    "tsx_gguf_find": (I32, [P, C.c_char_p, C.POINTER(GgufTensor)]),
+    "tsx_gguf_meta_count": (I32, [P]),
+    "tsx_gguf_meta_key": (C.c_char_p, [P, I32]),
+    "tsx_gguf_meta": (I32, [P, C.c_char_p, C.POINTER(C.c_int), C.POINTER(U64), C.POINTER(I64), C.POINTER(C.c_double),
+                            C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(U64)]),
+    "tsx_gguf_meta_item": (I32, [P, C.c_char_p, U64, C.POINTER(U64), C.POINTER(C.c_double), C.POINTER(C.c_char_p)]),
+    "tsx_gguf_layer_experts": (I32, [P, I32, I32, C.POINTER(GgufExperts)]),
+    "tsx_gguf_expert_blob": (I32, [C.POINTER(GgufExperts), I64, P]),
+    "tsx_gguf_upload_experts": (I32, [C.POINTER(GgufExperts), I64, I64, P, U64, P]),
+}
+
 _lib: C.CDLL | None = None
 
 
@@ -102,7 +152,7 @@ def lib() -> C.CDLL:
                 f"{LIB_PATH} is missing: build it with `python -m tinystrata_amd.build` (hipcc, gfx950)"
             )
         h = C.CDLL(str(LIB_PATH))
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in {**SIGNATURES, **GGUF_SIGNATURES}.items():
             f = getattr(h, name)
             f.restype = res
             f.argtypes = args

@@ -24,6 +24,7 @@ ARCH = os.environ.get("TSX_OFFLOAD_ARCH", "gfx950")
 SOURCES = [
     "tsx_abi.cpp",
     "tsx_weights.cpp",
+    "tsx_gguf.cpp",
     "strata_kernels.hip",
     "tsx_decode.hip",
     "tsx_layer.hip",
