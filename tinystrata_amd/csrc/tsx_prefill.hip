@@ -227,8 +227,13 @@ template <int T> constexpr int half_table_words() { return 2 * half_grid_words<T
 constexpr int lds_round(int bytes) { return (bytes + 15) / 16 * 16; }
 template <int T> constexpr int chunk_bytes() { return T == TSX_Q8_0 ? 8 * 34 : Fmt<T>::bytes; }
 // LDS bytes per row of a chunk's raw blocks: the block plus up to 15 bytes of alignment in front of it, rounded to
-// an odd number of 16-byte pieces so that 16 lanes reading the same field of 16 rows hit 16 different bank quads
-template <int T> constexpr int raw_stride() { return ((chunk_bytes<T>() + 15 + 15) / 16 | 1) * 16; }
+// an odd number of 16-byte pieces so that 16 lanes reading the same field of 16 rows hit 16 different bank quads.
+// A chunk of whole 16-byte pieces (Q4_K's 144 bytes, Q8_0's 272) always starts 16-byte aligned - rows, chunks and
+// experts are whole pieces apart - so it takes its own pieces only
+template <int T> constexpr bool chunk_aligned() { return chunk_bytes<T>() % 16 == 0; }
+template <int T> constexpr int raw_stride() {
+    return ((chunk_bytes<T>() + (chunk_aligned<T>() ? 0 : 15) + 15) / 16 | 1) * 16;
+}
 template <int T, int NW, int NB> constexpr int f16_lds_bytes() {
     return NB * (kBN * kBStride * 2 + kBN * 8 * 4 * (T == TSX_Q4_K ? 2 : 1)) + NW * 32 * raw_stride<T>() +
            half_table_words<T>() * 4 + NW * (32 * 4 + 8 * 32 * 4 * 3) + 64;
