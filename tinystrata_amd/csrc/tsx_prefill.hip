@@ -39,10 +39,31 @@ __host__ __device__ inline MmqPlanes planes(void* base, int64_t rows, int64_t co
     return p;
 }
 
+// zero codes and scales of the padding rows [rows, rows_pad) (a tile that over-reads them multiplies zeros), in the
+// quantize launch's last kPadBlocks blocks
+constexpr int kPadBlocks = 32;
+__device__ __forceinline__ void zero_pad_rows(const MmqPlanes& P, int64_t rows, int block) {
+    const int64_t nb = P.cols / 32;
+    const int64_t n_q = (P.rows_pad - rows) * P.cols, n_s = (P.rows_pad - rows) * nb;
+    const int64_t step = (int64_t) kPadBlocks * blockDim.x;
+    for (int64_t i = (int64_t) block * blockDim.x + threadIdx.x; i < n_q / 4; i += step)
+        ((uint32_t*) (P.q + rows * P.cols))[i] = 0u;  // rows * cols and cols are multiples of 32
+    for (int64_t i = (int64_t) block * blockDim.x + threadIdx.x; i < n_s; i += step) {
+        P.d[rows * nb + i] = 0.f;
+        P.m[rows * nb + i] = 0;
+    }
+}
+
 // 8 lanes per Q8_1 block, 4 values each (float4 loads, 4-byte code stores, DPP reductions within the 8 lanes):
-// row i of the output is row ids[i] (or i) of x.  The codes of q8_1_store32, byte for byte.
+// row i of the output is row ids[i] (or i) of x.  The codes of q8_1_store32, byte for byte.  Blocks past the
+// quantize's own zero the padding rows.
 __global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __restrict__ x, const int32_t* __restrict__ ids,
-                                                                MmqPlanes P, int64_t cols, int64_t ld, int64_t rows) {
+                                                                MmqPlanes P, int64_t cols, int64_t ld, int64_t rows,
+                                                                int qblocks) {
+    if ((int) blockIdx.x >= qblocks) {
+        zero_pad_rows(P, rows, (int) blockIdx.x - qblocks);
+        return;
+    }
     const int64_t nq = cols / 4;  // quads per row
     const int64_t qi = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     const bool valid = qi < rows * nq;
@@ -73,7 +94,12 @@ __global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __r
 
 // the same for rows that are not 16-byte aligned: one 32-lane group per Q8_1 block, one value per lane
 __global__ void __launch_bounds__(kThreads) mmq_quantize1_kernel(const float* __restrict__ x, const int32_t* __restrict__ ids,
-                                                                 MmqPlanes P, int64_t cols, int64_t ld, int64_t rows) {
+                                                                 MmqPlanes P, int64_t cols, int64_t ld, int64_t rows,
+                                                                 int qblocks) {
+    if ((int) blockIdx.x >= qblocks) {
+        zero_pad_rows(P, rows, (int) blockIdx.x - qblocks);
+        return;
+    }
     const int64_t nb = cols / 32;
     const int64_t gi = ((int64_t) blockIdx.x * blockDim.x + threadIdx.x) / 32;
     const int lane = threadIdx.x & 31;
@@ -97,18 +123,6 @@ __global__ void __launch_bounds__(kThreads) mmq_quantize1_kernel(const float* __
     if (lane == 0) {
         P.d[i * nb + b] = h2f(f2h(q8_1_finite(d)));
         P.m[i * nb + b] = qs;
-    }
-}
-
-// zero codes and scales of the padding rows [rows, rows_pad): a tile that over-reads them multiplies zeros
-__global__ void mmq_pad_kernel(MmqPlanes P, int64_t rows) {
-    const int64_t nb = P.cols / 32;
-    const int64_t n_q = (P.rows_pad - rows) * P.cols, n_s = (P.rows_pad - rows) * nb;
-    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n_q; i += (int64_t) gridDim.x * blockDim.x)
-        P.q[rows * P.cols + i] = 0;
-    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n_s; i += (int64_t) gridDim.x * blockDim.x) {
-        P.d[rows * nb + i] = 0.f;
-        P.m[rows * nb + i] = 0;
     }
 }
 
@@ -798,21 +812,15 @@ TSX_API int tsx_moe_mmq_quantize(const float* x, const int32_t* ids, void* xq, i
                 "tsx_moe_mmq_quantize: x, xq (256-byte aligned), cols a multiple of 32, ld >= cols");
     const MmqPlanes P = planes(xq, rows, cols);
     const hipStream_t s = (hipStream_t) stream;
-    if (rows > 0) {
-        if (aligned(x, 16) && ld % 4 == 0) {
-            const int64_t threads = rows * (cols / 4);
-            mmq_quantize_kernel<<<(unsigned) ((threads + kThreads - 1) / kThreads), kThreads, 0, s>>>(x, ids, P, cols, ld,
-                                                                                                      rows);
-        } else {
-            const int64_t threads = rows * (cols / 32) * 32;
-            mmq_quantize1_kernel<<<(unsigned) ((threads + kThreads - 1) / kThreads), kThreads, 0, s>>>(x, ids, P, cols, ld,
-                                                                                                       rows);
-        }
-        const int rc = launch_status("tsx_moe_mmq_quantize");
-        if (rc != TSX_OK) return rc;
+    // one launch: the quantize's blocks, then kPadBlocks that zero the padding rows
+    if (aligned(x, 16) && ld % 4 == 0) {
+        const int qb = (int) ((rows * (cols / 4) + kThreads - 1) / kThreads);
+        mmq_quantize_kernel<<<(unsigned) (qb + kPadBlocks), kThreads, 0, s>>>(x, ids, P, cols, ld, rows, qb);
+    } else {
+        const int qb = (int) ((rows * (cols / 32) * 32 + kThreads - 1) / kThreads);
+        mmq_quantize1_kernel<<<(unsigned) (qb + kPadBlocks), kThreads, 0, s>>>(x, ids, P, cols, ld, rows, qb);
     }
-    mmq_pad_kernel<<<64, kThreads, 0, s>>>(P, rows);
-    return launch_status("tsx_moe_mmq_quantize/pad");
+    return launch_status("tsx_moe_mmq_quantize");
 }
 
 TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {

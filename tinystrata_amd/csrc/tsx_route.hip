@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(256) group_kernel(const int32_t* __restrict__ 
 // the prompt sort, one block per tile of 1024 entries and no workspace: every block counts every entry (per expert:
 // all of them, and those of the tiles before its own), scans the totals into bounds, then scatters its own tile
 // stably - lanes of a wave that share an expert found with ballots, per-wave counts committed in wave order.
-constexpr int kSortThreads = 1024, kSortWaves = kSortThreads / 64;
+constexpr int kSortThreads = 1024, kSortWaves = kSortThreads / 64, kSortBatch = 8;
 // the lanes of the wave holding the same expert as this lane (x = -1 for none): a mask over the wave
 __device__ __forceinline__ uint64_t same_expert(int x) {
     uint64_t same = __ballot(1);
@@ -101,23 +101,43 @@ __global__ void __launch_bounds__(kSortThreads) route_sort_kernel(const int32_t*
                                                                   int32_t* __restrict__ ent_dst, int32_t* __restrict__ ent_tok,
                                                                   int32_t* __restrict__ rinv, int32_t* __restrict__ max_rows) {
     __shared__ int cnt[kMaxExperts], before[kMaxExperts], start[kMaxExperts];
-    __shared__ int wcnt[kSortWaves][kMaxExperts];
+    __shared__ int wcnt[kSortWaves][kMaxExperts], wbef[kSortWaves][kMaxExperts];
     __shared__ int s_wsum[kSortWaves], s_wmax[kSortWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile0 = blockIdx.x * kSortThreads;
-    for (int x = tid; x < n_expert; x += kSortThreads) cnt[x] = before[x] = 0;
-    for (int i = tid; i < kSortWaves * n_expert; i += kSortThreads) wcnt[i / n_expert][i % n_expert] = 0;
+    for (int i = tid; i < kSortWaves * n_expert; i += kSortThreads) wcnt[i / n_expert][i % n_expert] =
+        wbef[i / n_expert][i % n_expert] = 0;
     __syncthreads();
-    for (int base = 0; base < n_ent; base += kSortThreads) {  // a wave's 64 entries lie in one tile
-        const int e = base + tid;
-        int x = e < n_ent ? ids[e] : -1;
-        if (x < 0 || x >= n_expert) x = -1;  // an id out of range is dropped
-        const uint64_t same = same_expert(x);
-        if (x >= 0 && __builtin_popcountll(same & ((1ull << lane) - 1ull)) == 0) {
-            const int c = __builtin_popcountll(same);
-            atomicAdd(&cnt[x], c);
-            if (base < tile0) atomicAdd(&before[x], c);
+    // every entry's expert counted (a wave's 64 entries lie in one tile), kSortBatch tiles' ids requested at once so
+    // that one load latency covers them
+    for (int base = 0; base < n_ent; base += kSortThreads * kSortBatch) {
+        int xs[kSortBatch];
+#pragma unroll
+        for (int j = 0; j < kSortBatch; ++j) {
+            const int e = base + j * kSortThreads + tid;
+            xs[j] = e < n_ent ? ids[e] : -1;
         }
+#pragma unroll
+        for (int j = 0; j < kSortBatch; ++j) {
+            const int x = xs[j];
+            if (x >= 0 && x < n_expert) {  // an id out of range is dropped
+                // LDS atomics into the wave's own counts: no other wave touches them, and a wave's lanes share an
+                // expert a few times at most (a token picks an expert once)
+                atomicAdd(&wcnt[wave][x], 1);
+                if (base + j * kSortThreads < tile0) atomicAdd(&wbef[wave][x], 1);
+            }
+        }
+    }
+    __syncthreads();
+    for (int xx = tid; xx < n_expert; xx += kSortThreads) {  // the waves' counts summed (wcnt cleared for the scatter)
+        int c = 0, b = 0;
+        for (int w = 0; w < kSortWaves; ++w) {
+            c += wcnt[w][xx];
+            b += wbef[w][xx];
+            wcnt[w][xx] = 0;
+        }
+        cnt[xx] = c;
+        before[xx] = b;
     }
     __syncthreads();
     // bounds: exclusive scan of the counts over experts (expert x = thread x), and the largest count
