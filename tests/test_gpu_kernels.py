@@ -137,25 +137,29 @@ def test_combine(shared, n):
 
 
 @pytest.mark.parametrize("pad", [0, 1])  # rows 16-byte aligned (four values per lane), and not (one per lane)
-def test_mmq_quantize_planes_exact(pad):
+@pytest.mark.parametrize("rows", [70, 0])
+def test_mmq_quantize_planes_exact(pad, rows):
     rng = np.random.default_rng(8)
-    rows, cols = 70, 512
+    cols = 512
     xw = rng.normal(0, 1, (100, cols + pad)).astype(np.float32)
     xw[3, 32:64] = 0.0                               # an all-zero block
     x = xw[:, :cols]
     ids = rng.integers(0, 100, rows).astype(np.int32)
-    xq = host(ops.mmq_quantize(dev(xw), dev(ids), Q4_K, cols, cols + pad, rows))
+    # the planes start as garbage: the launch writes every row, the padding rows as zeros
+    xq0 = torch.full((ops.mmq_q8_bytes(rows, cols),), 0xAB, dtype=torch.uint8, device="cuda")
+    xq = host(ops.mmq_quantize(dev(xw), dev(ids), Q4_K, cols, cols + pad, rows, xq=xq0))
     rp = (rows + 63) // 64 * 64 + 64
     r256 = lambda v: (v + 255) // 256 * 256
     q = xq[: rp * cols].view(np.int8).reshape(rp, cols)
     d = xq[r256(rp * cols): r256(rp * cols) + rp * cols // 32 * 4].view(np.float32).reshape(rp, cols // 32)
     m0 = r256(rp * cols) + r256(rp * cols // 32 * 4)
     m = xq[m0: m0 + rp * cols // 32 * 4].view(np.int32).reshape(rp, cols // 32)
-    ed, _, ecodes = O.q8_1_split(O.quantize_q8_1(x[ids]))
-    assert (q[:rows].reshape(-1, 32) == ecodes).all()
-    assert (d[:rows].ravel() == ed).all()
-    assert (m[:rows].ravel() == ecodes.astype(np.int32).sum(1)).all()
-    assert (q[rows:] == 0).all() and (d[rows:] == 0).all()
+    if rows:
+        ed, _, ecodes = O.q8_1_split(O.quantize_q8_1(x[ids]))
+        assert (q[:rows].reshape(-1, 32) == ecodes).all()
+        assert (d[:rows].ravel() == ed).all()
+        assert (m[:rows].ravel() == ecodes.astype(np.int32).sum(1)).all()
+    assert (q[rows:] == 0).all() and (d[rows:] == 0).all() and (m[rows:] == 0).all()
 
 
 # ------------------------------------------------------------------ grouped experts
