@@ -89,11 +89,41 @@ TSX_API int tsx_moe_expert_grouped(const tsx_expert_layout* L, const uint64_t* g
                                    const int32_t* n_groups, const int32_t* ent_dst, const int32_t* ent_tok,
                                    int64_t cap_groups, int64_t cap_entries, const void* x_q8_1, void* scratch,
                                    float* out, void* stream, int64_t grid_groups);
-/* y[c][r] = W[r] . x[c] for ncols (1..8) columns of Q8_1 activations (n_in/32 blocks per column).
+/* y[c][r] = W[r] . x[c] for ncols (1..8) columns of Q8_1 activations (n_in/32 blocks per column).  Types: the expert
+ * formats (IQ3_XXS, IQ3_S, Q4_K, Q8_0) and Q4_0, Q6_K.
  * Replaces strata::kernels::iq_mmvq (include/strata/kernels/iq_kernels.hpp:27) and native_mmvq
  * (include/strata/kernels/native_mmvq.hpp:128-131): the shared expert's projections. */
 TSX_API int tsx_moe_mmvq(int type, const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                          void* stream);
+
+/* Several matrices of one format and shape in one launch, the matrices picked on the device: matrix j (j < count,
+ * count <= 65535) is table[ids[j]] + offset bytes, times the Q8_1 column x + (j / x_every) * x_stride bytes, into
+ * y + j * y_stride floats (n_out of them).  An id outside [0, n_table) gives zeros (the reference leaves it to the
+ * caller).  Types as tsx_moe_mmvq.  Replaces lfm_native_mmvq_ids / MmvqIds and lfm_native_mmvq_ids_supported
+ * (include/strata/lfm2/matvec.hpp:153-168; src/lfm2/matvec.cu:3134-3139): a decode step's routed experts with
+ * nothing of the host. */
+typedef struct {
+    const void* const* table; /* device array of matrix base pointers */
+    const int32_t* ids;       /* device [count] */
+    int32_t n_table;
+    uint64_t offset;
+    const void* x;
+    uint64_t x_stride;
+    int32_t x_every;
+    float* y;
+    uint64_t y_stride;
+} tsx_mmvq_ids;
+TSX_API int tsx_moe_mmvq_ids_supported(int type);
+TSX_API int tsx_moe_mmvq_ids(int type, const tsx_mmvq_ids* a, int count, int n_in, int n_out, void* stream);
+/* Up to 8 matrices given by the host: matrix j times its own column x[j] into y[j], as tsx_moe_mmvq(type, w[j], x[j],
+ * y[j], n_in, n_out, 1) would each.  Replaces lfm_native_mmvq_slots / MmvqSlots
+ * (include/strata/lfm2/matvec.hpp:146-152). */
+typedef struct {
+    const void* w[8];
+    const void* x[8];
+    float* y[8];
+} tsx_mmvq_slots;
+TSX_API int tsx_moe_mmvq_slots(int type, const tsx_mmvq_slots* a, int count, int n_in, int n_out, void* stream);
 
 /* The whole decode MoE layer for 1..8 tokens in two launches: routing (tsx_moe_router_topk's arithmetic), grouping,
  * Q8_1 of x, the grouped gate/up rows with SwiGLU + Q8_1, the down rows and the combine:

@@ -21,7 +21,8 @@ ORACLE_SO = HERE / "liboracle.so"
 REF_SO = HERE / "_ref" / "libref.so"
 
 Q8_0, Q8_1, Q4_K, Q8_K, IQ3_XXS, IQ3_S = 8, 9, 12, 15, 18, 21
-BLOCK = {Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q8_K: (256, 292), IQ3_XXS: (256, 98), IQ3_S: (256, 110)}
+BLOCK = {Q8_0: (32, 34), Q8_1: (32, 36), Q4_K: (256, 144), Q8_K: (256, 292), IQ3_XXS: (256, 98), IQ3_S: (256, 110),
+         2: (32, 18), 14: (256, 210)}  # Q4_0, Q6_K
 
 P, I32, I64, U64 = C.c_void_p, C.c_int, C.c_int64, C.c_uint64
 

@@ -236,14 +236,59 @@ static void q4k_sub(const uint8_t* blk, int j, int8_t w[32], int* sc, int* m, fl
     *dmin = orc_h2f(rd16(blk + 2));
 }
 
+/* Q6_K block -> 256 signed codes (code - 32) and the 16 signed scales, in ggml's dequantize_row_q6_K order: for each
+ * 128-value half, value l (0..31) of quarter q takes the low (q = 0, 1) or high (q = 2, 3) nibble of ql[l + 32 (q % 2)]
+ * and bits 2q, 2q + 1 of qh[l]; scale index = l / 16 + 2q (the reference reads the same layout,
+ * src/lfm2/matvec.cu:762-794) */
+static void q6k_block(const uint8_t* blk, int8_t v[256], int8_t sc[16]) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    for (int half = 0; half < 2; ++half) {
+        for (int l = 0; l < 32; ++l) {
+            const int h = qh[32 * half + l];
+            v[128 * half + l] = (int8_t) (((ql[64 * half + l] & 0xF) | ((h & 3) << 4)) - 32);
+            v[128 * half + l + 32] = (int8_t) (((ql[64 * half + l + 32] & 0xF) | (((h >> 2) & 3) << 4)) - 32);
+            v[128 * half + l + 64] = (int8_t) (((ql[64 * half + l] >> 4) | (((h >> 4) & 3) << 4)) - 32);
+            v[128 * half + l + 96] = (int8_t) (((ql[64 * half + l + 32] >> 4) | (((h >> 6) & 3) << 4)) - 32);
+        }
+    }
+    memcpy(sc, blk + 192, 16);
+}
+
 /* One sub-block (32 values) of a row: integer weights and the float pieces of its scale.
- * value(i) = a * w[i] - b (b only for Q4_K) */
-typedef struct { int8_t w[32]; double a, b; int isc, mn; float d, dmin; } sub_t;
+ * value(i) = a * k(i) * w[i] - b, k(i) = k16[i / 16] (1 except Q6_K), b only for Q4_K; Q4_0's w are the raw codes
+ * 0..15 and its value a * (w[i] - 8) */
+typedef struct { int8_t w[32]; double a, b; int isc, mn; float d, dmin; int k16[2]; } sub_t;
 
 static int decode_sub(int type, const uint8_t* row, int64_t u, sub_t* s) {
     s->b = 0.0;
     s->mn = 0;
+    s->k16[0] = s->k16[1] = 1;
     switch (type) {
+        case TSX_Q4_0: {
+            const uint8_t* blk = row + u * 18;
+            for (int i = 0; i < 16; ++i) {
+                s->w[i] = (int8_t) (blk[2 + i] & 15);
+                s->w[16 + i] = (int8_t) (blk[2 + i] >> 4);
+            }
+            s->d = orc_h2f(rd16(blk));
+            s->isc = 1;
+            s->a = s->d;
+            return 0;
+        }
+        case TSX_Q6_K: {
+            const uint8_t* blk = row + (u / 8) * 210;
+            int8_t v[256], sc[16];
+            q6k_block(blk, v, sc);
+            const int j = (int) (u % 8);
+            memcpy(s->w, v + 32 * j, 32);
+            s->k16[0] = sc[2 * j];
+            s->k16[1] = sc[2 * j + 1];
+            s->d = orc_h2f(rd16(blk + 208));
+            s->isc = 1;
+            s->a = s->d;
+            return 0;
+        }
         case TSX_IQ3_XXS: {
             const uint8_t* blk = row + (u / 8) * 98;
             iq3xxs_sub(blk, (int) (u % 8), s->w, &s->isc, &s->d);
@@ -276,21 +321,31 @@ static int decode_sub(int type, const uint8_t* row, int64_t u, sub_t* s) {
 }
 
 ORC_API int orc_dequantize(int type, const void* w, int64_t n, float* out) {
-    if (!tsx_weight_type_ok(type) || n % tsx_type_qk(type) != 0) return -1;
+    if (!tsx_mmvq_type_ok(type) || n % tsx_type_qk(type) != 0) return -1;
     const uint8_t* p = (const uint8_t*) w;
     for (int64_t u = 0; u < n / 32; ++u) {
         sub_t s;
         decode_sub(type, p, u, &s);
-        for (int i = 0; i < 32; ++i) out[u * 32 + i] = (float) (s.a * s.w[i] - s.b);
+        const int off = type == TSX_Q4_0 ? 8 : 0;
+        for (int i = 0; i < 32; ++i) out[u * 32 + i] = (float) (s.a * s.k16[i / 16] * (s.w[i] - off) - s.b);
     }
     return 0;
+}
+
+/* the exact integer sum of one sub-block against a Q8_1 block: sum k(i) w[i] a[i] (and sum a[i]) */
+static void sub_sums(const sub_t* s, const tsx_block_q8_1* a, int32_t* S, int32_t* M) {
+    int32_t lo = 0, hi = 0, m = 0;
+    for (int i = 0; i < 16; ++i) { lo += (int32_t) s->w[i] * a->qs[i]; m += a->qs[i]; }
+    for (int i = 16; i < 32; ++i) { hi += (int32_t) s->w[i] * a->qs[i]; m += a->qs[i]; }
+    *S = s->k16[0] * lo + s->k16[1] * hi;
+    *M = m;
 }
 
 /* ------------------------------------------------------------------ integer sums and dot products */
 /* sums[(r * ncols + c) * nsub + u] = S_u; qsums the same for M_u = sum a_int (null = not wanted) */
 ORC_API int orc_subblock_sums(int type, const void* w, int64_t n_in, int64_t n_rows, const void* xq, int64_t ncols,
                               int32_t* sums, int32_t* qsums) {
-    if (!tsx_weight_type_ok(type) || n_in % tsx_type_qk(type) != 0) return -1;
+    if (!tsx_mmvq_type_ok(type) || n_in % tsx_type_qk(type) != 0) return -1;
     const size_t rb = tsx_row_bytes(type, n_in);
     const int64_t nsub = n_in / 32;
     const tsx_block_q8_1* x = (const tsx_block_q8_1*) xq;
@@ -302,8 +357,8 @@ ORC_API int orc_subblock_sums(int type, const void* w, int64_t n_in, int64_t n_r
             decode_sub(type, row, u, &s);
             for (int64_t c = 0; c < ncols; ++c) {
                 const tsx_block_q8_1* a = x + c * nsub + u;
-                int32_t S = 0, M = 0;
-                for (int i = 0; i < 32; ++i) { S += (int32_t) s.w[i] * a->qs[i]; M += a->qs[i]; }
+                int32_t S, M;
+                sub_sums(&s, a, &S, &M);
                 sums[(r * ncols + c) * nsub + u] = S;
                 if (qsums) qsums[(r * ncols + c) * nsub + u] = M;
             }
@@ -314,7 +369,7 @@ ORC_API int orc_subblock_sums(int type, const void* w, int64_t n_in, int64_t n_r
 
 /* y[c * n_rows + r] = W[r] . x[c], Q8_1 activations */
 ORC_API int orc_mmvq_q8_1(int type, const void* w, int64_t n_in, int64_t n_rows, const void* xq, int64_t ncols, float* y) {
-    if (!tsx_weight_type_ok(type) || n_in % tsx_type_qk(type) != 0) return -1;
+    if (!tsx_mmvq_type_ok(type) || n_in % tsx_type_qk(type) != 0) return -1;
     const size_t rb = tsx_row_bytes(type, n_in);
     const int64_t nsub = n_in / 32;
     const tsx_block_q8_1* x = (const tsx_block_q8_1*) xq;
@@ -330,10 +385,13 @@ ORC_API int orc_mmvq_q8_1(int type, const void* w, int64_t n_in, int64_t n_rows,
                 decode_sub(type, row, u, &s);
                 for (int64_t c = 0; c < nc; ++c) {
                     const tsx_block_q8_1* a = x + (c0 + c) * nsub + u;
-                    int32_t S = 0, M = 0;
-                    for (int i = 0; i < 32; ++i) { S += (int32_t) s.w[i] * a->qs[i]; M += a->qs[i]; }
+                    int32_t S, M;
+                    sub_sums(&s, a, &S, &M);
                     const double d8 = orc_h2f(a->d);
-                    acc[c] += d8 * (s.a * S - s.b * M);
+                    if (type == TSX_Q4_0)  /* the reference's affine form with the block's stored sum */
+                        acc[c] += s.a * (S * d8 - 8.0 * orc_h2f(a->s));
+                    else
+                        acc[c] += d8 * (s.a * S - s.b * M);
                 }
             }
             for (int64_t c = 0; c < nc; ++c) y[(c0 + c) * n_rows + r] = (float) acc[c];

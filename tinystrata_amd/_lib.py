@@ -14,7 +14,7 @@ ABI_VERSION = 1
 TSX_OK, TSX_ERR_UNSUPPORTED, TSX_ERR_ARG, TSX_ERR_FORMAT, TSX_ERR_NOT_FOUND = 0, -1, -2, -3, -4
 
 # type ids (ggml's)
-Q8_0, Q8_1, Q4_K, Q8_K, IQ3_XXS, IQ3_S = 8, 9, 12, 15, 18, 21
+Q4_0, Q8_0, Q8_1, Q4_K, Q6_K, Q8_K, IQ3_XXS, IQ3_S = 2, 8, 9, 12, 14, 15, 18, 21
 
 
 class ExpertLayout(C.Structure):
@@ -51,6 +51,28 @@ class MmqProduct(C.Structure):
         ("dst", C.c_void_p),
         ("ld_dst", C.c_int64),
     ]
+
+
+class MmvqIds(C.Structure):
+    """tsx_mmvq_ids: matrices picked on the device through a table (reference MmvqIds)."""
+
+    _fields_ = [
+        ("table", C.c_void_p),
+        ("ids", C.c_void_p),
+        ("n_table", C.c_int32),
+        ("offset", C.c_uint64),
+        ("x", C.c_void_p),
+        ("x_stride", C.c_uint64),
+        ("x_every", C.c_int32),
+        ("y", C.c_void_p),
+        ("y_stride", C.c_uint64),
+    ]
+
+
+class MmvqSlots(C.Structure):
+    """tsx_mmvq_slots: up to 8 matrices given by the host (reference MmvqSlots)."""
+
+    _fields_ = [("w", C.c_void_p * 8), ("x", C.c_void_p * 8), ("y", C.c_void_p * 8)]
 
 
 class GgufTensor(C.Structure):
@@ -97,6 +119,9 @@ SIGNATURES = {
     "tsx_moe_swiglu_quantize_q8_1": (I32, [P, P, I64, P, P]),
     "tsx_moe_expert_grouped": (I32, [C.POINTER(ExpertLayout), P, P, P, P, P, I64, I64, P, P, P, P, I64]),
     "tsx_moe_mmvq": (I32, [I32, P, P, P, I32, I32, I32, P]),
+    "tsx_moe_mmvq_ids_supported": (I32, [I32]),
+    "tsx_moe_mmvq_ids": (I32, [I32, C.POINTER(MmvqIds), I32, I32, I32, P]),
+    "tsx_moe_mmvq_slots": (I32, [I32, C.POINTER(MmvqSlots), I32, I32, I32, P]),
     "tsx_moe_decode_layer_scratch_bytes": (SZ, [I32, I32, I64]),
     "tsx_moe_decode_layer": (I32, [C.POINTER(ExpertLayout), P, U64, I32, I32, I32, P, P, P, P, I32, P, P, P, P, P]),
     "tsx_moe_router_topk": (I32, [P, P, P, I32, I32, I32, P]),

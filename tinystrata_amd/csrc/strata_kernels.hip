@@ -94,11 +94,11 @@ void native_swiglu_quantize_q8_1(const float* gate, const float* up, void* x_q8_
     check_exit(tsx_moe_swiglu_quantize_q8_1(gate, up, (int64_t) n_in * ncols, x_q8_1, stream), "native_swiglu_quantize_q8_1");
 }
 
-bool native_mmvq_supported(int t) noexcept { return tsx_weight_type_ok(t) != 0; }
+bool native_mmvq_supported(int t) noexcept { return tsx_mmvq_type_ok(t) != 0; }
 
 std::size_t native_mmvq_weight_bytes(int t, int n_in, int n_out) {
     const size_t rb = tsx_row_bytes(t, n_in);
-    if (!tsx_weight_type_ok(t) || rb == 0) throw std::invalid_argument("native_mmvq_weight_bytes: unsupported type or width");
+    if (!tsx_mmvq_type_ok(t) || rb == 0) throw std::invalid_argument("native_mmvq_weight_bytes: unsupported type or width");
     return rb * (size_t) n_out;
 }
 
@@ -107,6 +107,34 @@ void native_mmvq(int t, const void* w, const void* x, float* y, int n_in, int n_
     const int rc = tsx_moe_mmvq(t, w, x, y, n_in, n_out, ncols, stream);
     if (rc == TSX_ERR_UNSUPPORTED || rc == TSX_ERR_ARG) throw std::invalid_argument(tsx_moe_last_error());
     if (rc != TSX_OK) throw std::runtime_error(tsx_moe_last_error());
+}
+
+bool lfm_native_mmvq_ids_supported(int t) { return tsx_moe_mmvq_ids_supported(t) != 0; }
+
+bool lfm_native_mmvq_ids(int t, const MmvqIds& m, int count, int n_in, int n_out, void* stream) {
+    if (!lfm_native_mmvq_ids_supported(t)) return false;
+    if (n_out <= 0 || count < 0 || count > 65535 || m.x_every <= 0)
+        throw std::invalid_argument("lfm_native_mmvq_ids requires n_out > 0, 1 to 65535 matrices and x_every > 0");
+    // the reference does not bound the ids: the table is taken as large as an int32 id can reach
+    const tsx_mmvq_ids a{m.table, m.ids, INT32_MAX, m.offset, m.x, m.x_stride, m.x_every, m.y, m.y_stride};
+    const int rc = tsx_moe_mmvq_ids(t, &a, count, n_in, n_out, stream);
+    if (rc == TSX_ERR_UNSUPPORTED) return false;
+    if (rc != TSX_OK) throw std::runtime_error(tsx_moe_last_error());
+    return true;
+}
+
+bool lfm_native_mmvq_slots(int t, const MmvqSlots& m, int count, int n_in, int n_out, void* stream) {
+    if (!lfm_native_mmvq_ids_supported(t)) return false;
+    tsx_mmvq_slots a{};
+    for (int j = 0; j < 8; ++j) {
+        a.w[j] = m.w[j];
+        a.x[j] = m.x[j];
+        a.y[j] = m.y[j];
+    }
+    const int rc = tsx_moe_mmvq_slots(t, &a, count, n_in, n_out, stream);
+    if (rc == TSX_ERR_UNSUPPORTED) return false;
+    if (rc != TSX_OK) throw std::runtime_error(tsx_moe_last_error());
+    return true;
 }
 
 bool native_router_topk_supported(int n_expert, int k) {

@@ -50,6 +50,28 @@ std::size_t native_mmvq_weight_bytes(int ggml_type, int n_in, int n_out);
 void native_mmvq(int ggml_type, const void* weights, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                  void* stream);
 
+// Several matrices of one format and shape in one launch (include/strata/lfm2/matvec.hpp:146-168): up to 8 given by
+// the host (MmvqSlots), or picked on the device through a table of matrix pointers (MmvqIds).  False, with nothing
+// launched, for a format there is no kernel for.
+struct MmvqSlots {
+    const void* w[8];
+    const void* x[8];
+    float* y[8];
+};
+bool lfm_native_mmvq_slots(int ggml_type, const MmvqSlots& slots, int count, int n_in, int n_out, void* stream);
+struct MmvqIds {
+    const void* const* table;
+    const int32_t* ids;
+    std::size_t offset;
+    const void* x;
+    std::size_t x_stride;
+    int x_every;
+    float* y;
+    std::size_t y_stride;
+};
+bool lfm_native_mmvq_ids_supported(int ggml_type);
+bool lfm_native_mmvq_ids(int ggml_type, const MmvqIds& ids, int count, int n_in, int n_out, void* stream);
+
 bool native_router_topk_supported(int n_expert, int k);
 void native_router_topk(const float* logits, int32_t* ids, float* weights, int n_expert, int k, int n_tok, void* stream);
 

@@ -166,6 +166,58 @@ __global__ void __launch_bounds__(kThreads) mmvq_kernel(const uint8_t* __restric
     }
 }
 
+// Several matrices of one format and shape (blockIdx.y = matrix j), one activation column each: y_j[r] = W_j[r] . x_j.
+// The matrices come from MatSource: a table indexed on the device (mmvq_ids) or up to 8 pointers (mmvq_slots).
+struct IdsSource {
+    const void* const* table;
+    const int32_t* ids;
+    int n_table;
+    uint64_t offset;
+    const uint8_t* x;
+    uint64_t x_stride;
+    int x_every;
+    float* y;
+    uint64_t y_stride;
+    __device__ bool at(int j, const uint8_t*& w, const tsx_block_q8_1*& xj, float*& yj) const {
+        const int id = ids[j];
+        yj = y + (uint64_t) j * y_stride;
+        if (id < 0 || id >= n_table) return false;
+        w = (const uint8_t*) table[id] + offset;
+        xj = (const tsx_block_q8_1*) (x + (uint64_t) (j / x_every) * x_stride);
+        return true;
+    }
+};
+struct SlotsSource {
+    const void* w[8];
+    const void* x[8];
+    float* y[8];
+    __device__ bool at(int j, const uint8_t*& wj, const tsx_block_q8_1*& xj, float*& yj) const {
+        wj = (const uint8_t*) w[j];
+        xj = (const tsx_block_q8_1*) x[j];
+        yj = y[j];
+        return true;
+    }
+};
+template <int T, int LPR, typename Src>
+__global__ void __launch_bounds__(kThreads) mmvq_many_kernel(Src src, uint64_t row_bytes, int n_in, int n_out) {
+    constexpr int RPW = kWave / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int slot = lane / LPR, l = lane % LPR;
+    const int r = (blockIdx.x * (kThreads / kWave) + wave) * RPW + slot;
+    if (r >= n_out) return;  // whole LPR groups leave together
+    const uint8_t* w = nullptr;
+    const tsx_block_q8_1* xj = nullptr;
+    float* yj = nullptr;
+    if (!src.at((int) blockIdx.y, w, xj, yj)) {  // an id outside the table: the matrix's outputs are zero
+        if (l == 0) yj[r] = 0.f;
+        return;
+    }
+    const tsx_block_q8_1* xs[1] = {xj};
+    float acc[1];
+    row_dots<T, LPR, 1>(w + (uint64_t) r * row_bytes, xs, 1, n_in / 32, l, acc);
+    if (l == 0) yj[r] = acc[0];
+}
+
 // the integer contract, one thread per (row, unit)
 template <int T>
 __global__ void __launch_bounds__(kThreads) subblock_sums_kernel(const uint8_t* __restrict__ w, uint64_t row_bytes,
@@ -221,7 +273,32 @@ int with_type(int type, F&& f) {
     }
 }
 
+// the formats of the single-matrix and id-indexed products
+template <typename F>
+int with_mmvq_type(int type, F&& f) {
+    switch (type) {
+        case TSX_Q4_0: return f(std::integral_constant<int, TSX_Q4_0>{});
+        case TSX_Q6_K: return f(std::integral_constant<int, TSX_Q6_K>{});
+        default: return with_type(type, f);
+    }
+}
+
 unsigned blocks_for(int64_t n, int per) { return (unsigned) ((n + per - 1) / per); }
+
+template <typename Src>
+int launch_many(const char* what, int type, const Src& src, int count, int n_in, int n_out, void* stream) {
+    const size_t rb = tsx_row_bytes(type, n_in);
+    const int lpr = lanes_per_row(n_in / 32), rows = (kThreads / kWave) * (kWave / lpr);
+    return with_mmvq_type(type, [&](auto T) {
+        return with_lpr(lpr, [&](auto LPR) {
+            const dim3 grid(blocks_for(n_out, rows), (unsigned) count);
+            mmvq_many_kernel<decltype(T)::value, decltype(LPR)::value, Src>
+                <<<grid, kThreads, 0, (hipStream_t) stream>>>(src, rb, n_in, n_out);
+            return launch_status(what);
+        });
+    });
+}
+
 
 }  // namespace
 }  // namespace tsx
@@ -301,7 +378,7 @@ TSX_API int tsx_moe_expert_grouped(const tsx_expert_layout* Lp, const uint64_t* 
 TSX_API int tsx_moe_mmvq(int type, const void* w, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                          void* stream) {
     const size_t rb = tsx_row_bytes(type, n_in);
-    if (!tsx_weight_type_ok(type) || rb == 0) {
+    if (!tsx_mmvq_type_ok(type) || rb == 0) {
         set_error("tsx_moe_mmvq: type %d with %d values per row not supported", type, n_in);
         return TSX_ERR_UNSUPPORTED;
     }
@@ -309,7 +386,7 @@ TSX_API int tsx_moe_mmvq(int type, const void* w, const void* x_q8_1, float* y, 
                 "tsx_moe_mmvq: w, x, y and 1..8 columns");
     if (n_out == 0) return TSX_OK;
     const int lpr = lanes_per_row(n_in / 32), rows = (kThreads / kWave) * (kWave / lpr);
-    return with_type(type, [&](auto T) {
+    return with_mmvq_type(type, [&](auto T) {
         return with_lpr(lpr, [&](auto LPR) {
             mmvq_kernel<decltype(T)::value, decltype(LPR)::value><<<blocks_for(n_out, rows), kThreads, 0, (hipStream_t) stream>>>(
                 (const uint8_t*) w, rb, (const tsx_block_q8_1*) x_q8_1, y, n_in, n_out, ncols);
@@ -318,10 +395,45 @@ TSX_API int tsx_moe_mmvq(int type, const void* w, const void* x_q8_1, float* y, 
     });
 }
 
+TSX_API int tsx_moe_mmvq_ids_supported(int type) { return tsx_mmvq_type_ok(type); }
+
+TSX_API int tsx_moe_mmvq_ids(int type, const tsx_mmvq_ids* a, int count, int n_in, int n_out, void* stream) {
+    if (!tsx_mmvq_type_ok(type) || tsx_row_bytes(type, n_in) == 0) {
+        set_error("tsx_moe_mmvq_ids: type %d with %d values per row not supported", type, n_in);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    TSX_REQUIRE(a && a->table && a->ids && a->x && a->y && a->n_table >= 0 && a->x_every > 0 && n_out > 0 &&
+                    count >= 0 && count <= 65535 && aligned(a->x, 4) && a->x_stride % 4 == 0,
+                "tsx_moe_mmvq_ids: table, ids, x (4-byte aligned, x_stride a multiple of 4), y, x_every > 0, n_out > 0 "
+                "and 0..65535 matrices");
+    if (count == 0) return TSX_OK;
+    const IdsSource src{a->table, a->ids, a->n_table, a->offset, (const uint8_t*) a->x, a->x_stride, a->x_every,
+                        a->y, a->y_stride};
+    return launch_many("tsx_moe_mmvq_ids", type, src, count, n_in, n_out, stream);
+}
+
+TSX_API int tsx_moe_mmvq_slots(int type, const tsx_mmvq_slots* a, int count, int n_in, int n_out, void* stream) {
+    if (!tsx_mmvq_type_ok(type) || tsx_row_bytes(type, n_in) == 0) {
+        set_error("tsx_moe_mmvq_slots: type %d with %d values per row not supported", type, n_in);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    TSX_REQUIRE(a && count >= 0 && count <= 8 && n_out > 0, "tsx_moe_mmvq_slots: slots, 0..8 matrices, n_out > 0");
+    SlotsSource src{};
+    for (int j = 0; j < count; ++j) {
+        TSX_REQUIRE(a->w[j] && a->x[j] && a->y[j] && aligned(a->x[j], 4), "tsx_moe_mmvq_slots: slot %d: w, x (4-byte "
+                                                                          "aligned), y", j);
+        src.w[j] = a->w[j];
+        src.x[j] = a->x[j];
+        src.y[j] = a->y[j];
+    }
+    if (count == 0) return TSX_OK;
+    return launch_many("tsx_moe_mmvq_slots", type, src, count, n_in, n_out, stream);
+}
+
 TSX_API int tsx_moe_subblock_sums(int type, const void* w, int64_t n_in, int64_t n_rows, const void* x_q8_1,
                                   int64_t ncols, int32_t* sums, int32_t* qsums, void* stream) {
     const size_t rb = tsx_row_bytes(type, n_in);
-    if (!tsx_weight_type_ok(type) || rb == 0) {
+    if (!tsx_mmvq_type_ok(type) || rb == 0) {
         set_error("tsx_moe_subblock_sums: type %d with %lld values per row not supported", type, (long long) n_in);
         return TSX_ERR_UNSUPPORTED;
     }
@@ -329,7 +441,7 @@ TSX_API int tsx_moe_subblock_sums(int type, const void* w, int64_t n_in, int64_t
                 "tsx_moe_subblock_sums: w, x, sums");
     const int nu = (int) (n_in / 32);
     if (n_rows == 0) return TSX_OK;
-    return with_type(type, [&](auto T) {
+    return with_mmvq_type(type, [&](auto T) {
         subblock_sums_kernel<decltype(T)::value><<<blocks_for(n_rows * nu, kThreads), kThreads, 0, (hipStream_t) stream>>>(
             (const uint8_t*) w, rb, nu, n_rows, (const tsx_block_q8_1*) x_q8_1, ncols, sums, qsums);
         return launch_status("tsx_moe_subblock_sums");

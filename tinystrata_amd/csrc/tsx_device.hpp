@@ -162,6 +162,7 @@ __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint
 struct Unit {
     int w[8];
     float a, b;
+    int k0, k1;  // Q6_K: the integer scales of the unit's two 16-value halves
 };
 
 template <int T> struct Fmt;
@@ -169,6 +170,8 @@ template <> struct Fmt<TSX_IQ3_XXS> { static constexpr int upb = 8, bytes = 98; 
 template <> struct Fmt<TSX_IQ3_S> { static constexpr int upb = 8, bytes = 110; };
 template <> struct Fmt<TSX_Q4_K> { static constexpr int upb = 8, bytes = 144; };
 template <> struct Fmt<TSX_Q8_0> { static constexpr int upb = 1, bytes = 34; };
+template <> struct Fmt<TSX_Q4_0> { static constexpr int upb = 1, bytes = 18; };
+template <> struct Fmt<TSX_Q6_K> { static constexpr int upb = 8, bytes = 210; };
 
 
 template <typename Tab>
@@ -243,23 +246,59 @@ __device__ __forceinline__ void unit_load_q80(const uint8_t* row, int u, Unit& o
     o.b = 0.f;
 }
 
+// Q4_0: the 4-bit codes as they are (0..15); the -8 offset is applied with the activation block's sum
+__device__ __forceinline__ void unit_load_q40(const uint8_t* row, int u, Unit& o) {
+    const uint8_t* blk = row + u * 18;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t q = ld32a2(blk + 2 + 4 * k);
+        o.w[k] = (int) (q & 0x0F0F0F0Fu);              // values 4k .. 4k + 3
+        o.w[4 + k] = (int) ((q >> 4) & 0x0F0F0F0Fu);   // values 16 + 4k ..
+    }
+    o.a = h2f((uint16_t) ld16(blk));
+    o.b = 0.f;
+}
+
+// Q6_K unit u = half u / 4, quarter u % 4 of the block: value l (0..31) of the quarter is the low (quarters 0, 1)
+// or high (2, 3) nibble of ql[64 half + 32 (quarter % 2) + l] with bits 2 quarter .. 2 quarter + 1 of
+// qh[32 half + l] above it, minus 32; the scale of values 0-15 is scales[8 half + 2 quarter], of 16-31 the next.
+// The codes stay unsigned (0..63): the -32 is applied with each half's activation sum
+__device__ __forceinline__ void unit_load_q6k(const uint8_t* row, int u, Unit& o) {
+    const uint8_t* blk = row + (u >> 3) * 210;
+    const int j = u & 7, half = j >> 2, qt = j & 3;
+    const uint8_t* ql = blk + 64 * half + 32 * (qt & 1);
+    const uint8_t* qh = blk + 128 + 32 * half;
+    const int lsh = 4 * (qt >> 1), hsh = 2 * qt;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        o.w[k] = (int) (((ld32a2(ql + 4 * k) >> lsh) & 0x0F0F0F0Fu) | (((ld32a2(qh + 4 * k) >> hsh) & 0x03030303u) << 4));
+    const int8_t* sc = (const int8_t*) (blk + 192 + 8 * half + 2 * qt);
+    o.k0 = sc[0];
+    o.k1 = sc[1];
+    o.a = h2f((uint16_t) ld16(blk + 208));
+    o.b = 0.f;
+}
+
 // unit u of a row of format T; g: where the codebooks are read (GridRef or RepTab<T>)
 template <int T, typename Tab>
 __device__ __forceinline__ void unit_load(const uint8_t* row, int u, Unit& o, const Tab& g) {
     if constexpr (T == TSX_IQ3_XXS) unit_load_iq3xxs(row, u, o, g);
     else if constexpr (T == TSX_IQ3_S) unit_load_iq3s(row, u, o, g);
     else if constexpr (T == TSX_Q4_K) unit_load_q4k(row, u, o);
+    else if constexpr (T == TSX_Q4_0) unit_load_q40(row, u, o);
+    else if constexpr (T == TSX_Q6_K) unit_load_q6k(row, u, o);
     else unit_load_q80(row, u, o);
 }
 
-// one Q8_1 activation block: d and the 32 codes as 8 words
+// one Q8_1 activation block: d, the sum field s and the 32 codes as 8 words
 struct Act {
     int q[8];
-    float d;
+    float d, s;
 };
 __device__ __forceinline__ void act_load(const tsx_block_q8_1* x, Act& a) {
     const uint32_t* p = (const uint32_t*) x;
     a.d = h2f((uint16_t) (p[0] & 0xFFFFu));
+    a.s = h2f((uint16_t) (p[0] >> 16));
 #pragma unroll
     for (int k = 0; k < 8; ++k) a.q[k] = (int) p[1 + k];
 }
@@ -267,11 +306,29 @@ __device__ __forceinline__ void act_load(const tsx_block_q8_1* x, Act& a) {
 // the unit's contribution to a row . activation dot product; *S (and *M) the exact integer sums
 template <int T>
 __device__ __forceinline__ float unit_dot(const Unit& w, const Act& x, int& S, int& M) {
+    if constexpr (T == TSX_Q6_K) {
+        // S = k0 * sum over values 0-15 of (code - 32) * a + k1 * the same over 16-31, exact in int32
+        int s0 = 0, s1 = 0, m0 = 0, m1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            s0 = dot4(w.w[k], x.q[k], s0);
+            s1 = dot4(w.w[4 + k], x.q[4 + k], s1);
+            m0 = dot4(0x01010101, x.q[k], m0);
+            m1 = dot4(0x01010101, x.q[4 + k], m1);
+        }
+        S = w.k0 * (s0 - 32 * m0) + w.k1 * (s1 - 32 * m1);
+        M = m0 + m1;
+        return x.d * (w.a * (float) S);
+    }
     int s = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) s = dot4(w.w[k], x.q[k], s);
     S = s;
-    if constexpr (T == TSX_Q4_K) {
+    if constexpr (T == TSX_Q4_0) {
+        // the reference's affine form: d_w (S d_x - 8 s_x) with the activation block's sum field s_x
+        M = 0;
+        return w.a * ((float) s * x.d - 8.0f * x.s);
+    } else if constexpr (T == TSX_Q4_K) {
         int m = 0;
 #pragma unroll
         for (int k = 0; k < 8; ++k) m = dot4(0x01010101, x.q[k], m);

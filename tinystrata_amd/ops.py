@@ -11,7 +11,7 @@ import ctypes as C
 import numpy as np
 import torch
 
-from ._lib import IQ3_S, IQ3_XXS, Q4_K, Q8_0, ExpertLayout, MmqProduct, check, lib
+from ._lib import IQ3_S, IQ3_XXS, Q4_K, Q8_0, ExpertLayout, MmqProduct, MmvqIds, MmvqSlots, check, lib
 
 WEIGHT_TYPES = (Q8_0, Q4_K, IQ3_XXS, IQ3_S)
 Q8_1_BLOCK_BYTES = 36
@@ -92,6 +92,28 @@ def iq_mmvq(ggml_type: int, w, x_q8_1, n_in: int, n_out: int, ncols: int, y=None
 
 
 native_mmvq = iq_mmvq
+
+
+def mmvq_ids_supported(ggml_type: int) -> bool:
+    return bool(lib().tsx_moe_mmvq_ids_supported(ggml_type))
+
+
+def mmvq_ids(ggml_type: int, table: torch.Tensor, ids: torch.Tensor, offset: int, x_q8_1, x_stride: int, x_every: int,
+             y: torch.Tensor, y_stride: int, count: int, n_in: int, n_out: int, stream=None) -> torch.Tensor:
+    """Matrix j = table[ids[j]] + offset bytes (table: int64 device addresses), times the Q8_1 column
+    x + (j / x_every) * x_stride bytes, into y + j * y_stride floats (reference lfm_native_mmvq_ids)."""
+    a = MmvqIds(table=_p(table), ids=_p(ids), n_table=table.numel(), offset=offset, x=_p(x_q8_1), x_stride=x_stride,
+                x_every=x_every, y=_p(y), y_stride=y_stride)
+    check(lib().tsx_moe_mmvq_ids(ggml_type, C.byref(a), count, n_in, n_out, _stream(stream)), "mmvq_ids")
+    return y
+
+
+def mmvq_slots(ggml_type: int, ws, xs, ys, n_in: int, n_out: int, stream=None) -> None:
+    """Up to 8 matrices ws[j] times their own Q8_1 column xs[j] into ys[j] (reference lfm_native_mmvq_slots)."""
+    a = MmvqSlots()
+    for j, (w, x, y) in enumerate(zip(ws, xs, ys)):
+        a.w[j], a.x[j], a.y[j] = _p(w), _p(x), _p(y)
+    check(lib().tsx_moe_mmvq_slots(ggml_type, C.byref(a), len(ws), n_in, n_out, _stream(stream)), "mmvq_slots")
 
 
 def decode_layer_scratch_bytes(n_tok: int, k: int, n_ff: int) -> int:
