@@ -158,6 +158,16 @@ TSX_API int tsx_moe_router_topk(const float* logits, int32_t* ids, float* weight
 TSX_API int tsx_moe_group(const int32_t* ids, int n_ent, int k, int n_expert, const void* blobs, uint64_t stride,
                           uint64_t* grp_ptr, int32_t* grp_start, int32_t* n_groups, int32_t* ent_dst,
                           int32_t* ent_tok, void* stream);
+/* tsx_moe_group for a hybrid layer: only the entries whose expert has an HBM slot (slot_of[x] >= 0; slot_of is
+ * n_expert device ints) are grouped, and group g's blob is slot slot_of[x] of `slots` (stride bytes apart).
+ * Replaces k_group_hy (src/qwen35/q36_engine.cu:423-452). */
+TSX_API int tsx_moe_group_resident(const int32_t* ids, int n_ent, int k, int n_expert, const int32_t* slot_of,
+                                   const void* slots, uint64_t stride, uint64_t* grp_ptr, int32_t* grp_start,
+                                   int32_t* n_groups, int32_t* ent_dst, int32_t* ent_tok, void* stream);
+/* Row e of parts (n floats) = row miss[e] of rows where miss[e] >= 0, else unchanged: the CPU's rows of a hybrid
+ * layer merged into the GPU's before the combine.  Replaces k_merge_cpu (src/qwen35/q36_engine.cu:455-460, called at :3205) in the compact form. */
+TSX_API int tsx_moe_merge_rows(float* parts, const float* rows, const int32_t* miss, int n_ent, int64_t n,
+                               void* stream);
 /* The prompt's entries sorted by expert: bounds[x]..bounds[x+1] are expert x's sorted rows (n_expert + 1 ints);
  * sorted row r holds entry ent_dst[r] of token ent_tok[r]; rinv[e] = entry e's sorted row; *max_rows = the most
  * rows of one expert.  Rows inside an expert are in entry order.  All on the device (no host round trip).

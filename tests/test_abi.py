@@ -38,6 +38,16 @@ def test_every_gguf_symbol_is_exported_and_bound():
     assert sorted(_lib.GGUF_SIGNATURES) == names
 
 
+def test_every_pool_symbol_is_exported_and_bound():
+    names = sorted(set(re.findall(r"TSX_API\s+[\w\s\*]+?\b(tsx_(?:cpu|pool|moe)_\w+)\s*\(",
+                                  (ROOT / "include" / "tsx_pool.h").read_text())))
+    assert len(names) >= 14
+    lib = _lib.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(_lib.POOL_SIGNATURES) == names
+
+
 def test_abi_handshake():
     lib = _lib.lib()
     v = lib.tsx_moe_abi()

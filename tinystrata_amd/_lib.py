@@ -11,7 +11,8 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libtsx_moe.so"
 
 ABI_VERSION = 1
-TSX_OK, TSX_ERR_UNSUPPORTED, TSX_ERR_ARG, TSX_ERR_FORMAT, TSX_ERR_NOT_FOUND = 0, -1, -2, -3, -4
+TSX_OK, TSX_ERR_UNSUPPORTED, TSX_ERR_ARG, TSX_ERR_FORMAT, TSX_ERR_NOT_FOUND, TSX_ERR_STALLED = 0, -1, -2, -3, -4, -5
+CPU_MAXT, POOL_MAX_SPLIT = 8, 96  # tokens per CPU job, experts per pool batch (include/tsx_pool.h)
 
 # type ids (ggml's)
 Q4_0, Q8_0, Q8_1, Q4_K, Q6_K, Q8_K, IQ3_XXS, IQ3_S = 2, 8, 9, 12, 14, 15, 18, 21
@@ -105,6 +106,38 @@ class GgufExperts(C.Structure):
 
 P, I32, I64, U64, SZ = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_size_t
 
+class CpuFmt(C.Structure):
+    """tsx_cpu_fmt: one layer's expert geometry on the CPU (reference NativeFmt)."""
+
+    _fields_ = [
+        ("gu_type", C.c_int32),
+        ("d_type", C.c_int32),
+        ("gu_act", C.c_int32),
+        ("d_act", C.c_int32),
+        ("n_embd", C.c_int64),
+        ("n_ff", C.c_int64),
+        ("gu_row", C.c_uint64),
+        ("d_row", C.c_uint64),
+        ("up_off", C.c_uint64),
+        ("down_off", C.c_uint64),
+        ("bytes", C.c_uint64),
+        ("act_bytes", C.c_uint64),
+        ("h_bytes", C.c_uint64),
+    ]
+
+
+class CpuJob(C.Structure):
+    """tsx_cpu_job: one expert applied to up to 8 tokens (reference ExpertJobMulti)."""
+
+    _fields_ = [
+        ("blob", C.c_void_p),
+        ("nt", C.c_int32),
+        ("pad", C.c_int32),
+        ("out", C.c_void_p * CPU_MAXT),
+        ("act", C.c_void_p * CPU_MAXT),
+    ]
+
+
 # name -> (restype, argtypes); the list is the whole C ABI, checked against include/tsx_moe.h by the tests
 SIGNATURES = {
     "tsx_moe_abi": (I32, []),
@@ -126,6 +159,8 @@ SIGNATURES = {
     "tsx_moe_decode_layer": (I32, [C.POINTER(ExpertLayout), P, U64, I32, I32, I32, P, P, P, P, I32, P, P, P, P, P]),
     "tsx_moe_router_topk": (I32, [P, P, P, I32, I32, I32, P]),
     "tsx_moe_group": (I32, [P, I32, I32, I32, P, U64, P, P, P, P, P, P]),
+    "tsx_moe_group_resident": (I32, [P, I32, I32, I32, P, P, U64, P, P, P, P, P, P]),
+    "tsx_moe_merge_rows": (I32, [P, P, P, I32, I64, P]),
     "tsx_moe_route_sort": (I32, [P, I32, I32, I32, P, P, P, P, P, P]),
     "tsx_moe_combine": (I32, [P, P, P, P, I32, P, P, I32, I32, I32, P]),
     "tsx_moe_mmq_q8_bytes": (SZ, [I64, I64]),
@@ -159,6 +194,24 @@ GGUF_SIGNATURES = {
     "tsx_gguf_upload_experts": (I32, [C.POINTER(GgufExperts), I64, I64, P, U64, P]),
 }
 
+# the CPU expert rows, the pool and the hybrid split of include/tsx_pool.h
+POOL_SIGNATURES = {
+    "tsx_cpu_fmt_init": (I32, [I32, I32, I64, I64, C.POINTER(CpuFmt)]),
+    "tsx_cpu_quant_act": (I32, [C.POINTER(CpuFmt), P, P]),
+    "tsx_cpu_quant_h": (I32, [C.POINTER(CpuFmt), P, P]),
+    "tsx_cpu_gu_rows": (I32, [C.POINTER(CpuFmt), P, C.POINTER(P), I32, C.POINTER(P), I32, I32]),
+    "tsx_cpu_down_rows": (I32, [C.POINTER(CpuFmt), P, C.POINTER(P), I32, C.POINTER(P), I32, I32]),
+    "tsx_pool_create": (I32, [I32, I32, I32, I32, C.POINTER(P)]),
+    "tsx_pool_destroy": (None, [P]),
+    "tsx_pool_workers": (I32, [P]),
+    "tsx_pool_host_works": (I32, [P]),
+    "tsx_pool_run": (I32, [P, C.POINTER(CpuFmt), C.POINTER(CpuJob), I32]),
+    "tsx_pool_stats": (I32, [P, C.POINTER(C.c_double), C.POINTER(I64)]),
+    "tsx_pool_set_spin_us": (I32, [P, I64]),
+    "tsx_pool_set_stall_ms": (I32, [P, I64]),
+    "tsx_moe_hybrid_cpu": (I32, [P, C.POINTER(CpuFmt), P, U64, P, I32, I32, I32, P, P, P, P, P]),
+}
+
 _lib: C.CDLL | None = None
 
 
@@ -177,7 +230,7 @@ def lib() -> C.CDLL:
                 f"{LIB_PATH} is missing: build it with `python -m tinystrata_amd.build` (hipcc, gfx950)"
             )
         h = C.CDLL(str(LIB_PATH))
-        for name, (res, args) in {**SIGNATURES, **GGUF_SIGNATURES}.items():
+        for name, (res, args) in {**SIGNATURES, **GGUF_SIGNATURES, **POOL_SIGNATURES}.items():
             f = getattr(h, name)
             f.restype = res
             f.argtypes = args

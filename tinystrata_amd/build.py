@@ -25,6 +25,8 @@ SOURCES = [
     "tsx_abi.cpp",
     "tsx_weights.cpp",
     "tsx_gguf.cpp",
+    "tsx_cpu_rows.cpp",
+    "tsx_pool.cpp",
     "strata_kernels.hip",
     "tsx_decode.hip",
     "tsx_layer.hip",

@@ -1,0 +1,330 @@
+// tsx_cpu_rows.cpp - one routed expert's rows on the CPU, for the hybrid CPU/GPU split: experts without a slot in
+// HBM run here while the GPU runs the resident ones.
+//
+// Reference: strata::kernels::cpu::native_gu_rows / native_down_rows / native_quant_act / native_quant_h
+// (include/strata/kernels/cpu/native_expert.hpp:41-65; src/kernels/cpu/native_expert.cpp:147-299) and the
+// multi-token IQ rows (src/kernels/cpu/iq_avx512.cpp:108-186): a weight block is decoded once and dotted with every
+// token of the job.  The activations here are Q8_1 (the GPU kernels' contract), not ggml's vec_dot_type, so a miss
+// served by the CPU has the same integer sub-block sums S_j = sum w_int * a_int as it would on the GPU.
+//
+// Per row and token: acc = sum over 32-value units u (in order) of d8_u * (a_u * S_u - b_u * M_u) in double, with
+// a_u the unit's weight scale (d * (2 ls + 1) / 4 for IQ3_XXS, d * (2 ls + 1) for IQ3_S, d * sc for Q4_K, d for
+// Q8_0), b_u = dmin * m (Q4_K, else 0) and M_u the unit's sum of activation codes; the row's value is (float) acc.
+// The integer dot of a unit is one AVX2 maddubs chain where the CPU has AVX2, else a scalar loop (same integers).
+#pragma STDC FP_CONTRACT OFF
+
+#include <immintrin.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "tsx_common.hpp"
+#include "tsx_half.hpp"
+#include "tsx_pool.h"
+
+namespace tsx {
+namespace {
+
+constexpr int kQ8_1 = 9;
+
+inline uint16_t rd16(const uint8_t* p) {
+    uint16_t v;
+    std::memcpy(&v, p, 2);
+    return v;
+}
+inline uint32_t rd32(const uint8_t* p) {
+    uint32_t v;
+    std::memcpy(&v, p, 4);
+    return v;
+}
+
+// ------------------------------------------------------------------ integer dot of 32 int8 pairs
+int dot32_scalar(const int8_t* w, const int8_t* a) {
+    int s = 0;
+    for (int i = 0; i < 32; ++i) s += (int) w[i] * (int) a[i];
+    return s;
+}
+// |w| (unsigned) times a with w's sign, pairs summed to int16 (|w| <= 128, |a| <= 127: no saturation), then to int32
+__attribute__((target("avx2"))) int dot32_avx2(const int8_t* w, const int8_t* a) {
+    const __m256i vw = _mm256_loadu_si256((const __m256i*) w), va = _mm256_loadu_si256((const __m256i*) a);
+    const __m256i p16 = _mm256_maddubs_epi16(_mm256_sign_epi8(vw, vw), _mm256_sign_epi8(va, vw));
+    const __m256i p32 = _mm256_madd_epi16(p16, _mm256_set1_epi16(1));
+    const __m128i s4 = _mm_add_epi32(_mm256_castsi256_si128(p32), _mm256_extracti128_si256(p32, 1));
+    const __m128i s2 = _mm_add_epi32(s4, _mm_shuffle_epi32(s4, 0x4E));
+    const __m128i s1 = _mm_add_epi32(s2, _mm_shuffle_epi32(s2, 0xB1));
+    return _mm_cvtsi128_si32(s1);
+}
+using Dot32 = int (*)(const int8_t*, const int8_t*);
+Dot32 pick_dot32() { return __builtin_cpu_supports("avx2") ? dot32_avx2 : dot32_scalar; }
+const Dot32 g_dot32 = pick_dot32();
+
+// ------------------------------------------------------------------ weight units
+// Up to 8 units (one 256-value block, or one 32-value Q8_0 block): int8 weights and the double scale pieces
+struct Units {
+    alignas(32) int8_t w[8][32];
+    double a[8], b[8];
+    int n;
+};
+
+inline uint32_t sign_byte_xxs(uint32_t v7) { return v7 | ((uint32_t) __builtin_popcount(v7) & 1u) << 7; }
+
+void put_word(int8_t* dst, uint32_t g, uint32_t signs4) {  // 4 grid bytes with 4 sign bits
+    for (int i = 0; i < 4; ++i) {
+        const int v = (int) ((g >> (8 * i)) & 0xFFu);
+        dst[i] = (int8_t) (((signs4 >> i) & 1u) ? -v : v);
+    }
+}
+
+// block `blk` of a row of `type` -> its units
+void decode_block(int type, const uint8_t* blk, Units& U) {
+    switch (type) {
+        case TSX_IQ3_XXS: {  // {d; qs[64] grid indices; 8 x u32: 4 x 7 sign bits, 4-bit scale}
+            const double d = (double) h2f(rd16(blk));
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t aux = rd32(blk + 66 + 4 * j);
+                for (int l = 0; l < 4; ++l) {
+                    const uint32_t s8 = sign_byte_xxs((aux >> (7 * l)) & 127u);
+                    put_word(U.w[j] + 8 * l, tsx_iq3xxs_word(blk[2 + 8 * j + 2 * l]), s8 & 15u);
+                    put_word(U.w[j] + 8 * l + 4, tsx_iq3xxs_word(blk[2 + 8 * j + 2 * l + 1]), s8 >> 4);
+                }
+                U.a[j] = d * 0.25 * (int) (2 * (aux >> 28) + 1);
+                U.b[j] = 0.0;
+            }
+            U.n = 8;
+            return;
+        }
+        case TSX_IQ3_S: {  // {d; qs[64]; qh[8]; signs[32]; scales[4]}
+            const double d = (double) h2f(rd16(blk));
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t qh = blk[66 + j];
+                for (int q = 0; q < 8; ++q) {
+                    const int idx = (int) (blk[2 + 8 * j + q] | ((qh >> q) & 1u) << 8);
+                    put_word(U.w[j] + 4 * q, tsx_iq3s_word(idx), (uint32_t) (blk[74 + 4 * j + q / 2] >> (4 * (q & 1))));
+                }
+                U.a[j] = d * (int) (2 * ((blk[106 + j / 2] >> (4 * (j & 1))) & 15u) + 1);
+                U.b[j] = 0.0;
+            }
+            U.n = 8;
+            return;
+        }
+        case TSX_Q4_K: {  // {d, dmin; scales[12] (6-bit sc, m); qs[128]}
+            const float d = h2f(rd16(blk)), dmin = h2f(rd16(blk + 2));
+            const uint8_t* sc = blk + 4;
+            for (int j = 0; j < 8; ++j) {
+                int s, m;
+                if (j < 4) {
+                    s = sc[j] & 63;
+                    m = sc[j + 4] & 63;
+                } else {
+                    s = (sc[j + 4] & 15) | (sc[j - 4] >> 6) << 4;
+                    m = (sc[j + 4] >> 4) | (sc[j] >> 6) << 4;
+                }
+                const uint8_t* qs = blk + 16 + 32 * (j / 2);
+                for (int i = 0; i < 32; ++i) U.w[j][i] = (int8_t) ((j & 1) ? qs[i] >> 4 : qs[i] & 15);
+                U.a[j] = (double) d * s;
+                U.b[j] = (double) dmin * m;
+            }
+            U.n = 8;
+            return;
+        }
+        default: {  // Q8_0 {d; qs[32]}
+            std::memcpy(U.w[0], blk + 2, 32);
+            U.a[0] = (double) h2f(rd16(blk));
+            U.b[0] = 0.0;
+            U.n = 1;
+            return;
+        }
+    }
+}
+
+// y[t] = row . act[t] for nt tokens; n_in values (whole blocks of the type)
+void row_dot(int type, const uint8_t* row, int64_t n_in, const uint8_t* const* act, int nt, float* y,
+             const double* const* d8, const int* const* msum) {
+    const int qk = type == TSX_Q8_0 ? 32 : 256;
+    const size_t bb = tsx_type_block_bytes(type);
+    const bool q4k = type == TSX_Q4_K;
+    double acc[TSX_CPU_MAXT];
+    for (int t = 0; t < nt; ++t) acc[t] = 0.0;
+    Units U;
+    for (int64_t blk = 0; blk < n_in / qk; ++blk) {
+        decode_block(type, row + blk * bb, U);
+        const int64_t u0 = blk * (qk / 32);
+        for (int j = 0; j < U.n; ++j) {
+            const int64_t u = u0 + j;
+            for (int t = 0; t < nt; ++t) {
+                const int S = g_dot32(U.w[j], (const int8_t*) (act[t] + 36 * u + 4));
+                const int M = q4k ? msum[t][u] : 0;
+                acc[t] += d8[t][u] * (U.a[j] * S - U.b[j] * M);
+            }
+        }
+    }
+    for (int t = 0; t < nt; ++t) y[t] = (float) acc[t];
+}
+
+// per-token unit scales and code sums of nt Q8_1 rows of nu units (the caller's buffers)
+void unpack_acts(const void* const* act, int nt, int64_t nu, bool sums, double* d8, int* ms, const double** pd,
+                 const int** pm) {
+    for (int t = 0; t < nt; ++t) {
+        const uint8_t* a = (const uint8_t*) act[t];
+        for (int64_t u = 0; u < nu; ++u) {
+            d8[t * nu + u] = (double) h2f(rd16(a + 36 * u));
+            if (sums) {
+                int s = 0;
+                for (int i = 0; i < 32; ++i) s += (int8_t) a[36 * u + 4 + i];
+                ms[t * nu + u] = s;
+            }
+        }
+        pd[t] = d8 + t * nu;
+        pm[t] = ms + t * nu;
+    }
+}
+
+inline float q8_1_finite(float v) { return std::fabs(v) > 65504.0f ? std::copysign(65504.0f, v) : v; }
+
+// Q8_1 of n values: per 32, the largest magnitude and the sum by a 32-lane xor butterfly (the order of the GPU
+// quantizers' reductions), d = amax / 127, codes round(x / d) within +-127 (0 when amax is 0)
+void quant_q8_1(const float* x, int64_t n, uint8_t* dst) {
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const float* xb = x + 32 * b;
+        float am[32], sm[32], ta[32], ts[32];
+        for (int l = 0; l < 32; ++l) {
+            am[l] = std::fabs(xb[l]);
+            sm[l] = xb[l];
+        }
+        for (int o = 16; o > 0; o >>= 1) {
+            for (int l = 0; l < 32; ++l) {
+                ta[l] = std::fmax(am[l], am[l ^ o]);
+                ts[l] = sm[l] + sm[l ^ o];
+            }
+            std::memcpy(am, ta, sizeof am);
+            std::memcpy(sm, ts, sizeof sm);
+        }
+        const float amax = am[0], d = q8_1_finite(amax / 127.0f);
+        uint8_t* y = dst + 36 * b;
+        for (int l = 0; l < 32; ++l) {
+            int q = 0;
+            if (amax != 0.0f) {
+                const float r = std::round(xb[l] / d);
+                q = (int) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
+            }
+            y[4 + l] = (uint8_t) (int8_t) q;
+        }
+        const uint16_t hd = f2h(q8_1_finite(d)), hs = f2h(q8_1_finite(sm[0]));
+        std::memcpy(y, &hd, 2);
+        std::memcpy(y + 2, &hs, 2);
+    }
+}
+
+bool fmt_ok(const tsx_cpu_fmt* f) { return f && f->gu_act == kQ8_1 && f->d_act == kQ8_1 && f->n_embd > 0; }
+
+}  // namespace
+
+// the rows of one phase, shared with the pool
+int cpu_gu_rows(const tsx_cpu_fmt& f, const uint8_t* blob, const void* const* act, int nt, float* const* ff, int r0,
+                int r1) {
+    const int64_t N = f.n_embd, nu = N / 32;
+    const bool q4k = f.gu_type == TSX_Q4_K;
+    double d8[TSX_CPU_MAXT * 512];
+    int ms[TSX_CPU_MAXT * 512];
+    if (nu > 512) return TSX_ERR_UNSUPPORTED;
+    const double* pd[TSX_CPU_MAXT];
+    const int* pm[TSX_CPU_MAXT];
+    unpack_acts(act, nt, nu, q4k, d8, ms, pd, pm);
+    const uint8_t* const* a = (const uint8_t* const*) act;
+    float g[TSX_CPU_MAXT], u[TSX_CPU_MAXT];
+    for (int r = r0; r < r1; ++r) {
+        row_dot(f.gu_type, blob + (uint64_t) r * f.gu_row, N, a, nt, g, pd, pm);
+        row_dot(f.gu_type, blob + f.up_off + (uint64_t) r * f.gu_row, N, a, nt, u, pd, pm);
+        for (int t = 0; t < nt; ++t) {
+            const float s = g[t] / (1.0f + std::exp(-g[t]));
+            ff[t][r] = s * u[t];
+        }
+    }
+    return TSX_OK;
+}
+
+int cpu_down_rows(const tsx_cpu_fmt& f, const uint8_t* blob, const void* const* hq, int nt, float* const* out,
+                  int r0, int r1) {
+    const int64_t FF = f.n_ff, nu = FF / 32;
+    const bool q4k = f.d_type == TSX_Q4_K;
+    double d8[TSX_CPU_MAXT * 256];
+    int ms[TSX_CPU_MAXT * 256];
+    if (nu > 256) return TSX_ERR_UNSUPPORTED;
+    const double* pd[TSX_CPU_MAXT];
+    const int* pm[TSX_CPU_MAXT];
+    unpack_acts(hq, nt, nu, q4k, d8, ms, pd, pm);
+    const uint8_t* const* a = (const uint8_t* const*) hq;
+    float y[TSX_CPU_MAXT];
+    for (int r = r0; r < r1; ++r) {
+        row_dot(f.d_type, blob + f.down_off + (uint64_t) r * f.d_row, FF, a, nt, y, pd, pm);
+        for (int t = 0; t < nt; ++t) out[t][r] = y[t];
+    }
+    return TSX_OK;
+}
+
+void cpu_quant(const float* x, int64_t n, void* dst) { quant_q8_1(x, n, (uint8_t*) dst); }
+
+}  // namespace tsx
+
+using namespace tsx;
+
+extern "C" {
+
+TSX_API int tsx_cpu_fmt_init(int gu_type, int d_type, int64_t n_embd, int64_t n_ff, tsx_cpu_fmt* f) {
+    clear_error();
+    TSX_REQUIRE(f != nullptr, "tsx_cpu_fmt_init: null output");
+    auto ok = [](int t) { return t == TSX_IQ3_XXS || t == TSX_IQ3_S || t == TSX_Q4_K || t == TSX_Q8_0; };
+    if (!ok(gu_type) || !ok(d_type) || n_embd <= 0 || n_ff <= 0 || n_embd % 256 || n_ff % 256 || n_embd > 16384 ||
+        n_ff > 8192) {
+        set_error("tsx_cpu_fmt_init: types %d/%d, n_embd %lld, n_ff %lld not supported (expert types; multiples of "
+                  "256; n_embd <= 16384, n_ff <= 8192)", gu_type, d_type, (long long) n_embd, (long long) n_ff);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    tsx_expert_layout L;
+    if (tsx_moe_expert_layout(gu_type, d_type, n_embd, n_ff, &L) != TSX_OK) return TSX_ERR_UNSUPPORTED;
+    f->gu_type = gu_type;
+    f->d_type = d_type;
+    f->gu_act = f->d_act = kQ8_1;
+    f->n_embd = n_embd;
+    f->n_ff = n_ff;
+    f->gu_row = L.gu_row;
+    f->d_row = L.d_row;
+    f->up_off = L.up_off;
+    f->down_off = L.down_off;
+    f->bytes = L.bytes;
+    f->act_bytes = (uint64_t) (n_embd / 32) * 36;
+    f->h_bytes = (uint64_t) (n_ff / 32) * 36;
+    return TSX_OK;
+}
+
+TSX_API int tsx_cpu_quant_act(const tsx_cpu_fmt* f, const float* x, void* dst) {
+    clear_error();
+    TSX_REQUIRE(fmt_ok(f) && x && dst, "tsx_cpu_quant_act: format, x and dst");
+    cpu_quant(x, f->n_embd, dst);
+    return TSX_OK;
+}
+
+TSX_API int tsx_cpu_quant_h(const tsx_cpu_fmt* f, const float* h, void* dst) {
+    clear_error();
+    TSX_REQUIRE(fmt_ok(f) && h && dst, "tsx_cpu_quant_h: format, h and dst");
+    cpu_quant(h, f->n_ff, dst);
+    return TSX_OK;
+}
+
+TSX_API int tsx_cpu_gu_rows(const tsx_cpu_fmt* f, const uint8_t* blob, const void* const* act, int nt,
+                            float* const* ff, int r0, int r1) {
+    clear_error();
+    TSX_REQUIRE(fmt_ok(f) && blob && act && ff && nt >= 1 && nt <= TSX_CPU_MAXT && 0 <= r0 && r0 <= r1 &&
+                    r1 <= f->n_ff, "tsx_cpu_gu_rows: format, blob, 1..8 tokens, 0 <= r0 <= r1 <= n_ff");
+    return cpu_gu_rows(*f, blob, act, nt, ff, r0, r1);
+}
+
+TSX_API int tsx_cpu_down_rows(const tsx_cpu_fmt* f, const uint8_t* blob, const void* const* hq, int nt,
+                              float* const* out, int r0, int r1) {
+    clear_error();
+    TSX_REQUIRE(fmt_ok(f) && blob && hq && out && nt >= 1 && nt <= TSX_CPU_MAXT && 0 <= r0 && r0 <= r1 &&
+                    r1 <= f->n_embd, "tsx_cpu_down_rows: format, blob, 1..8 tokens, 0 <= r0 <= r1 <= n_embd");
+    return cpu_down_rows(*f, blob, hq, nt, out, r0, r1);
+}
+
+}  // extern "C"

@@ -28,13 +28,17 @@ __global__ void __launch_bounds__(256) router_topk_kernel(const float* __restric
 __global__ void __launch_bounds__(256) group_kernel(const int32_t* __restrict__ ids, int n_ent, int k, int n_expert,
                                                     const uint8_t* blobs, uint64_t stride, uint64_t* __restrict__ grp_ptr,
                                                     int32_t* __restrict__ grp_start, int32_t* __restrict__ n_groups,
-                                                    int32_t* __restrict__ ent_dst, int32_t* __restrict__ ent_tok) {
+                                                    int32_t* __restrict__ ent_dst, int32_t* __restrict__ ent_tok,
+                                                    const int32_t* __restrict__ slot_of) {
+    // slot_of (may be null): expert x's blob is slot slot_of[x] of `blobs`, and entries of experts without a slot
+    // (slot_of[x] < 0) are left out; null: expert x's blob is blob x
     __shared__ int cnt[kMaxExperts], off[kMaxExperts];
+    auto grouped = [&](int x) { return x >= 0 && x < n_expert && (!slot_of || slot_of[x] >= 0); };
     for (int x = threadIdx.x; x < n_expert; x += blockDim.x) cnt[x] = 0;
     __syncthreads();
     for (int e = threadIdx.x; e < n_ent; e += blockDim.x) {
         const int x = ids[e];
-        if (x >= 0 && x < n_expert) atomicAdd(&cnt[x], 1);
+        if (grouped(x)) atomicAdd(&cnt[x], 1);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -42,7 +46,7 @@ __global__ void __launch_bounds__(256) group_kernel(const int32_t* __restrict__ 
         for (int x = 0; x < n_expert; ++x) {
             off[x] = pos;
             if (cnt[x] == 0) continue;
-            grp_ptr[g] = (uint64_t) (blobs + (uint64_t) x * stride);
+            grp_ptr[g] = (uint64_t) (blobs + (uint64_t) (slot_of ? slot_of[x] : x) * stride);
             grp_start[g] = pos;
             pos += cnt[x];
             ++g;
@@ -58,7 +62,7 @@ __global__ void __launch_bounds__(256) group_kernel(const int32_t* __restrict__ 
             if (wave == w) {
                 const int e = base + w * 64 + lane;
                 int x = e < n_ent ? ids[e] : -1;
-                const bool ok = x >= 0 && x < n_expert;
+                const bool ok = grouped(x);
                 if (!ok) x = -1;  // one class for every invalid id: -1 differs from 0..511 in bit 9
                 uint64_t same = __ballot(1);
 #pragma unroll
@@ -194,6 +198,17 @@ __global__ void __launch_bounds__(kSortThreads) route_sort_kernel(const int32_t*
 }
 
 // x[t][i] += sum_j w_j parts[p(t,j)][i] (first product, then FMA, pick order) + sigmoid(sgate) * shared[t][i]
+// row e of parts = row miss[e] of rows where miss[e] >= 0 (an entry the CPU computed), else unchanged
+// (reference k_merge_cpu, src/qwen35/q36_engine.cu:455-460, with compact row indices)
+__global__ void __launch_bounds__(256) merge_rows_kernel(float* __restrict__ parts, const float* __restrict__ rows,
+                                                         const int32_t* __restrict__ miss, int64_t n) {
+    const int e = blockIdx.y;
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int m = miss[e];
+    if (m < 0 || i >= n) return;
+    parts[(int64_t) e * n + i] = rows[(int64_t) m * n + i];
+}
+
 __global__ void __launch_bounds__(256) combine_kernel(float* __restrict__ x, const float* __restrict__ parts,
                                                       const int32_t* __restrict__ prow, const float* __restrict__ wts, int k,
                                                       const float* __restrict__ shared, const float* __restrict__ sgate,
@@ -275,8 +290,31 @@ TSX_API int tsx_moe_group(const int32_t* ids, int n_ent, int k, int n_expert, co
     TSX_REQUIRE(ids && grp_ptr && grp_start && n_groups && ent_dst && ent_tok && n_ent >= 0 && k >= 1,
                 "tsx_moe_group: a null pointer or a bad count");
     group_kernel<<<1, 256, 0, (hipStream_t) stream>>>(ids, n_ent, k, n_expert, (const uint8_t*) blobs, stride, grp_ptr,
-                                                      grp_start, n_groups, ent_dst, ent_tok);
+                                                      grp_start, n_groups, ent_dst, ent_tok, nullptr);
     return launch_status("tsx_moe_group");
+}
+
+TSX_API int tsx_moe_group_resident(const int32_t* ids, int n_ent, int k, int n_expert, const int32_t* slot_of,
+                                   const void* slots, uint64_t stride, uint64_t* grp_ptr, int32_t* grp_start,
+                                   int32_t* n_groups, int32_t* ent_dst, int32_t* ent_tok, void* stream) {
+    if (n_expert <= 0 || n_expert > kMaxExperts) {
+        set_error("tsx_moe_group_resident: %d experts (at most 512)", n_expert);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    TSX_REQUIRE(ids && slot_of && slots && grp_ptr && grp_start && n_groups && ent_dst && ent_tok && n_ent >= 0 &&
+                    k >= 1, "tsx_moe_group_resident: a null pointer or a bad count");
+    group_kernel<<<1, 256, 0, (hipStream_t) stream>>>(ids, n_ent, k, n_expert, (const uint8_t*) slots, stride,
+                                                      grp_ptr, grp_start, n_groups, ent_dst, ent_tok, slot_of);
+    return launch_status("tsx_moe_group_resident");
+}
+
+TSX_API int tsx_moe_merge_rows(float* parts, const float* rows, const int32_t* miss, int n_ent, int64_t n,
+                               void* stream) {
+    TSX_REQUIRE(parts && rows && miss && n_ent >= 0 && n >= 0, "tsx_moe_merge_rows: parts, rows, miss, sizes");
+    if (n_ent == 0 || n == 0) return TSX_OK;
+    merge_rows_kernel<<<dim3((unsigned) ((n + 255) / 256), (unsigned) n_ent), 256, 0, (hipStream_t) stream>>>(
+        parts, rows, miss, n);
+    return launch_status("tsx_moe_merge_rows");
 }
 
 TSX_API int tsx_moe_route_sort(const int32_t* ids, int n_ent, int k, int n_expert, int32_t* bounds, int32_t* ent_dst,

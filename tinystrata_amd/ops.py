@@ -156,6 +156,21 @@ def group_entries(ids: torch.Tensor, k: int, n_expert: int, blobs_ptr: int, stri
     return bufs
 
 
+def group_resident(ids: torch.Tensor, k: int, n_expert: int, slot_of: torch.Tensor, slots_ptr: int, stride: int,
+                   bufs, stream=None):
+    """Decode grouping of a hybrid layer (k_group_hy): only entries whose expert has a slot; group blobs in slots."""
+    gp, gs, ng, ed, et = bufs
+    check(lib().tsx_moe_group_resident(_p(ids), ids.numel(), k, n_expert, _p(slot_of), slots_ptr, stride, _p(gp),
+                                       _p(gs), _p(ng), _p(ed), _p(et), _stream(stream)), "group_resident")
+    return bufs
+
+
+def merge_rows(parts: torch.Tensor, rows: torch.Tensor, miss: torch.Tensor, stream=None) -> None:
+    """parts[e] = rows[miss[e]] where miss[e] >= 0 (k_merge_cpu, compact rows)."""
+    n_ent, n = parts.shape
+    check(lib().tsx_moe_merge_rows(_p(parts), _p(rows), _p(miss), n_ent, n, _stream(stream)), "merge_rows")
+
+
 def route_sort(ids: torch.Tensor, k: int, n_expert: int, bufs=None, stream=None):
     """The prompt's expert sort: bounds [E+1], ent_dst, ent_tok, rinv [n_ent], max_rows [1]."""
     n_ent = ids.numel()
