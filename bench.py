@@ -42,6 +42,10 @@ CONFIGS = {
     "prefill_long": dict(gu=18, d=21, N=2048, FF=512, E=256, k=8, shared=True, T=4096, layers=4, route="zipf1.3",
                          outliers=True, desc="configs[4]: prefill 4096 tokens, 256 experts top-8 + shared, IQ3, "
                                               "Zipf(1.3) skew, 1% outlier channels x20"),
+    # not a BASELINE configuration: the hybrid CPU/GPU split on configs[1]'s layer, half of the experts in HBM
+    "hybrid": dict(gu=18, d=21, N=2048, FF=512, E=256, k=8, shared=True, T=1, layers=4, route="normal",
+                   resident=128, desc="hybrid: configs[1]'s decode layer with 128 of 256 experts in HBM, the rest "
+                                      "on the CPU pool"),
 }
 
 
@@ -84,6 +88,8 @@ def main() -> int:
     from tinystrata_amd import _lib, moe, ops
 
     cfg = CONFIGS[args.config]
+    if "resident" in cfg:
+        return run_hybrid(args, cfg)
     gu, d, N, FF, E, k, shared, T, layers = (cfg[key] for key in ("gu", "d", "N", "FF", "E", "k", "shared", "T", "layers"))
     prefill = T > 8
     dev = torch.device("cuda:0")
@@ -279,6 +285,73 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def run_hybrid(args, cfg) -> int:
+    """The hybrid decode layer (tinystrata_amd.pool.HybridMoELayer): eager steps of `layers` layers with distinct
+    weights, each with a host round trip (routing to the host, the CPU rows back), so no graph.  value = layer-tokens/s
+    of the whole layer; "pool" = the CPU pool's expert bytes per second over its drain time."""
+    import torch
+
+    from tinystrata_amd import _lib, moe, ops
+    from tinystrata_amd.pool import ExpertPool, HybridMoELayer
+
+    gu, d, N, FF, E, k, T, layers, R = (cfg[key] for key in ("gu", "d", "N", "FF", "E", "k", "T", "layers",
+                                                               "resident"))
+    dev = torch.device("cuda:0")
+    _lib.check(_lib.lib().tsx_moe_init(0), "tsx_moe_init")
+    L = ops.native_expert_layout(gu, d, N, FF)
+    distinct = 24
+    pool = moe.synthetic_pool(L, distinct, seed=1234)
+    pool_dev = torch.from_numpy(pool).to(dev)
+    rng = np.random.default_rng(7)
+    cpu = ExpertPool()
+    hys = []
+    for l in range(layers):
+        order = (rng.permutation(E) + l) % distinct
+        # the routed experts live in the host copy and the layer's slots only
+        W = moe.MoEWeights(L=L, n_expert=E, stride=pool.shape[1], blobs=torch.empty(0, dtype=torch.uint8, device=dev),
+                           shared=pool_dev[int(rng.integers(distinct))].clone())
+        hys.append(HybridMoELayer(W, np.ascontiguousarray(pool[order]), np.sort(rng.permutation(E)[:R]), k, T, dev,
+                                  cpu))
+    del pool_dev
+    x0 = torch.from_numpy(rng.normal(0, 1, (T, N)).astype(np.float32)).to(dev)
+    logits = torch.from_numpy(make_logits(rng, cfg, layers)).to(dev)
+    sg = torch.from_numpy(rng.normal(0, 1, (layers, T)).astype(np.float32)).to(dev)
+    x = torch.empty_like(x0)
+
+    def step():
+        x.copy_(x0)
+        for l in range(layers):
+            hys[l](x, logits[l], sg[l], x)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    st0 = cpu.stats()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    st1 = cpu.stats()
+    per_layer = dt / (args.steps * layers)
+    drain_s = (st1["drain"] - st0["drain"]) / 1e3
+    pool_gbs = (st1["bytes"] - st0["bytes"]) / drain_s / 1e9 if drain_s > 0 else None
+    misses = sum(h.n_miss for h in hys) / layers
+    print(json.dumps({
+        "metric": METRIC, "value": round(T / per_layer, 1), "unit": "layer-tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8 x int8 -> int32, fp32",
+        "data": "synthetic: random-init quantized experts, N(0,1) activations and logits",
+        "config": {"workload": cfg["desc"], "layer_us": round(per_layer * 1e6, 3), "n_tok": T,
+                   "layers": layers, "resident_experts": R, "experts": E, "cpu_entries_per_layer": misses},
+        "pool": {"workers": cpu.workers, "host_works": cpu.host_works, "expert_GBps": pool_gbs,
+                 "drain_ms_per_layer": round((st1["drain"] - st0["drain"]) / (args.steps * layers), 4)},
+        "roofline": None, "cpu_baseline": None,
+    }))
+    cpu.close()
     return 0
 
 

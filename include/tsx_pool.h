@@ -8,7 +8,8 @@
  * src/kernels/cpu/native_expert.cpp:50-126); the oracle's mode 1 reports that gap.
  *
  * Functions return TSX_OK, TSX_ERR_UNSUPPORTED, TSX_ERR_ARG, or TSX_ERR_STALLED (the pool saw no progress for the
- * stall limit; it then refuses further work).  tsx_moe_last_error() has the message.  Nothing here touches the GPU.
+ * stall limit; it then refuses further work).  tsx_moe_last_error() has the message.  Only
+ * tsx_moe_hybrid_decode_layer touches the GPU.
  */
 #ifndef TSX_POOL_H
 #define TSX_POOL_H
@@ -96,6 +97,50 @@ TSX_API int tsx_pool_set_stall_ms(tsx_pool* p, int64_t ms);
 TSX_API int tsx_moe_hybrid_cpu(tsx_pool* p, const tsx_cpu_fmt* f, const uint8_t* host_blobs, uint64_t stride,
                                const int32_t* slot_of, int n_expert, int k, int n_tok, const int32_t* ids,
                                const float* x, float* cpu_out, int32_t* miss, int32_t* n_miss);
+
+/* A whole hybrid decode layer in one call (reference moe_hybrid_gpu + moe_hybrid_cpu + the combine,
+ * src/qwen35/q36_engine.cu:3052-3209).  Enqueued on `stream`: routing, the ids and x to the pinned host buffers,
+ * the resident entries grouped into their slots and run, the shared expert; then the host waits for the ids and x
+ * alone and runs the misses on the pool while the GPU works, uploads the CPU rows and the miss map, merges them
+ * into `parts` and enqueues the combine (y += ...).  Returns after the last enqueue; n_miss is written.  The pinned
+ * buffers are reused by the next call on the same stream (its copies run after this call's uploads). */
+typedef struct tsx_hybrid_layer {
+    tsx_expert_layout L;
+    int32_t n_expert, k, n_tok, sg_stride;
+    const uint8_t* host_blobs; /* host: every expert, stride bytes apart */
+    uint64_t stride;
+    const int32_t* slot_of;    /* host [n_expert]: slot or -1 */
+    const int32_t* d_slot_of;  /* device copy of slot_of */
+    const void* slots;         /* device: the resident blobs, stride bytes apart */
+    const void* shared;        /* device: the shared expert's blob, or null */
+    const float* sgate;        /* device [n_tok * sg_stride] (with shared) */
+    const float* x;            /* device [n_tok][n_embd] */
+    const float* logits;       /* device [n_tok][n_expert] */
+    float* y;                  /* device [n_tok][n_embd], += */
+    int32_t* ids;              /* device [n_tok * k] */
+    float* wts;                /* device [n_tok * k] */
+    uint64_t* grp_ptr;         /* device: min(n_ent, n_expert) groups */
+    int32_t* grp_start;
+    int32_t* n_groups;
+    int32_t* ent_dst;
+    int32_t* ent_tok;
+    void* xq;                  /* device [n_tok][n_embd / 32 * 36] */
+    void* scratch;             /* device, tsx_moe_expert_scratch_bytes(n_ent, n_ff) */
+    float* parts;              /* device [n_ent][n_embd] */
+    float* sh_gate;            /* device [n_tok][n_ff] (with shared) */
+    float* sh_up;
+    void* sh_hq;               /* device [n_tok][n_ff / 32 * 36] */
+    float* sh_out;             /* device [n_tok][n_embd] */
+    int32_t* h_ids;            /* pinned host [n_tok * k] */
+    float* h_x;                /* pinned host [n_tok][n_embd] */
+    float* h_rows;             /* pinned host [n_ent][n_embd] */
+    int32_t* h_miss;           /* pinned host [n_ent] */
+    float* d_rows;             /* device [n_ent][n_embd] */
+    int32_t* d_miss;           /* device [n_ent] */
+    int32_t n_miss;            /* out */
+    int32_t pad;
+} tsx_hybrid_layer;
+TSX_API int tsx_moe_hybrid_decode_layer(tsx_pool* p, const tsx_cpu_fmt* f, tsx_hybrid_layer* a, void* stream);
 
 #ifdef __cplusplus
 }

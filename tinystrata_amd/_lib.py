@@ -138,6 +138,17 @@ class CpuJob(C.Structure):
     ]
 
 
+class HybridLayerArgs(C.Structure):
+    """tsx_hybrid_layer: the buffers of one hybrid decode layer call."""
+
+    _fields_ = [("L", ExpertLayout), ("n_expert", C.c_int32), ("k", C.c_int32), ("n_tok", C.c_int32),
+                ("sg_stride", C.c_int32)] + [(n, C.c_void_p) for n in (
+                    "host_blobs", "stride", "slot_of", "d_slot_of", "slots", "shared", "sgate", "x", "logits", "y",
+                    "ids", "wts", "grp_ptr", "grp_start", "n_groups", "ent_dst", "ent_tok", "xq", "scratch", "parts",
+                    "sh_gate", "sh_up", "sh_hq", "sh_out", "h_ids", "h_x", "h_rows", "h_miss", "d_rows",
+                    "d_miss")] + [("n_miss", C.c_int32), ("pad", C.c_int32)]
+
+
 # name -> (restype, argtypes); the list is the whole C ABI, checked against include/tsx_moe.h by the tests
 SIGNATURES = {
     "tsx_moe_abi": (I32, []),
@@ -210,6 +221,7 @@ POOL_SIGNATURES = {
     "tsx_pool_set_spin_us": (I32, [P, I64]),
     "tsx_pool_set_stall_ms": (I32, [P, I64]),
     "tsx_moe_hybrid_cpu": (I32, [P, C.POINTER(CpuFmt), P, U64, P, I32, I32, I32, P, P, P, P, P]),
+    "tsx_moe_hybrid_decode_layer": (I32, [P, C.POINTER(CpuFmt), C.POINTER(HybridLayerArgs), P]),
 }
 
 _lib: C.CDLL | None = None

@@ -45,7 +45,7 @@ int dot32_scalar(const int8_t* w, const int8_t* a) {
     return s;
 }
 // |w| (unsigned) times a with w's sign, pairs summed to int16 (|w| <= 128, |a| <= 127: no saturation), then to int32
-__attribute__((target("avx2"))) int dot32_avx2(const int8_t* w, const int8_t* a) {
+__attribute__((target("avx2"))) inline int dot32_avx2(const int8_t* w, const int8_t* a) {
     const __m256i vw = _mm256_loadu_si256((const __m256i*) w), va = _mm256_loadu_si256((const __m256i*) a);
     const __m256i p16 = _mm256_maddubs_epi16(_mm256_sign_epi8(vw, vw), _mm256_sign_epi8(va, vw));
     const __m256i p32 = _mm256_madd_epi16(p16, _mm256_set1_epi16(1));
@@ -54,9 +54,6 @@ __attribute__((target("avx2"))) int dot32_avx2(const int8_t* w, const int8_t* a)
     const __m128i s1 = _mm_add_epi32(s2, _mm_shuffle_epi32(s2, 0xB1));
     return _mm_cvtsi128_si32(s1);
 }
-using Dot32 = int (*)(const int8_t*, const int8_t*);
-Dot32 pick_dot32() { return __builtin_cpu_supports("avx2") ? dot32_avx2 : dot32_scalar; }
-const Dot32 g_dot32 = pick_dot32();
 
 // ------------------------------------------------------------------ weight units
 // Up to 8 units (one 256-value block, or one 32-value Q8_0 block): int8 weights and the double scale pieces
@@ -137,29 +134,124 @@ void decode_block(int type, const uint8_t* blk, Units& U) {
     }
 }
 
-// y[t] = row . act[t] for nt tokens; n_in values (whole blocks of the type)
-void row_dot(int type, const uint8_t* row, int64_t n_in, const uint8_t* const* act, int nt, float* y,
-             const double* const* d8, const int* const* msum) {
-    const int qk = type == TSX_Q8_0 ? 32 : 256;
-    const size_t bb = tsx_type_block_bytes(type);
-    const bool q4k = type == TSX_Q4_K;
-    double acc[TSX_CPU_MAXT];
-    for (int t = 0; t < nt; ++t) acc[t] = 0.0;
-    Units U;
-    for (int64_t blk = 0; blk < n_in / qk; ++blk) {
-        decode_block(type, row + blk * bb, U);
-        const int64_t u0 = blk * (qk / 32);
-        for (int j = 0; j < U.n; ++j) {
-            const int64_t u = u0 + j;
-            for (int t = 0; t < nt; ++t) {
-                const int S = g_dot32(U.w[j], (const int8_t*) (act[t] + 36 * u + 4));
-                const int M = q4k ? msum[t][u] : 0;
-                acc[t] += d8[t][u] * (U.a[j] * S - U.b[j] * M);
-            }
-        }
+// ------------------------------------------------------------------ the same units with AVX2
+// The grid words of a unit come from one 8-lane gather; the 32 sign bits (byte v / 8, bit v % 8 for value v) become
+// a byte mask m, and w = (g ^ m) - m negates where it is set.
+struct HostGrids {
+    uint32_t xxs[256], s[512];
+    HostGrids() {
+        for (int i = 0; i < 256; ++i) xxs[i] = tsx_iq3xxs_word(i);
+        for (int i = 0; i < 512; ++i) s[i] = tsx_iq3s_word(i);
     }
-    for (int t = 0; t < nt; ++t) y[t] = (float) acc[t];
+};
+const HostGrids g_grids;
+
+__attribute__((target("avx2"))) inline __m256i sign_mask(uint32_t sw) {
+    const __m256i sel = _mm256_setr_epi8(0, 0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, 1, 2, 2, 2, 2, 2, 2, 2, 2, 3, 3,
+                                         3, 3, 3, 3, 3, 3);
+    const __m256i bit = _mm256_set1_epi64x((long long) 0x8040201008040201ULL);
+    const __m256i v = _mm256_shuffle_epi8(_mm256_set1_epi32((int) sw), sel);
+    return _mm256_cmpeq_epi8(_mm256_and_si256(v, bit), bit);
 }
+__attribute__((target("avx2"))) inline void put_unit(int8_t* dst, __m256i g, uint32_t sw) {
+    const __m256i m = sign_mask(sw);
+    _mm256_store_si256((__m256i*) dst, _mm256_sub_epi8(_mm256_xor_si256(g, m), m));
+}
+
+__attribute__((target("avx2"))) inline void decode_block_avx2(int type, const uint8_t* blk, Units& U) {
+    switch (type) {
+        case TSX_IQ3_XXS: {
+            const double d = (double) h2f(rd16(blk));
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t aux = rd32(blk + 66 + 4 * j);
+                const __m256i idx = _mm256_cvtepu8_epi32(_mm_loadl_epi64((const __m128i*) (blk + 2 + 8 * j)));
+                const __m256i g = _mm256_i32gather_epi32((const int*) g_grids.xxs, idx, 4);
+                uint32_t sw = 0;
+                for (int l = 0; l < 4; ++l) sw |= sign_byte_xxs((aux >> (7 * l)) & 127u) << (8 * l);
+                put_unit(U.w[j], g, sw);
+                U.a[j] = d * 0.25 * (int) (2 * (aux >> 28) + 1);
+                U.b[j] = 0.0;
+            }
+            U.n = 8;
+            return;
+        }
+        case TSX_IQ3_S: {
+            const double d = (double) h2f(rd16(blk));
+            const __m256i shifts = _mm256_setr_epi32(0, 1, 2, 3, 4, 5, 6, 7);
+            for (int j = 0; j < 8; ++j) {
+                const __m256i lo = _mm256_cvtepu8_epi32(_mm_loadl_epi64((const __m128i*) (blk + 2 + 8 * j)));
+                const __m256i hi = _mm256_and_si256(_mm256_srlv_epi32(_mm256_set1_epi32(blk[66 + j]), shifts),
+                                                    _mm256_set1_epi32(1));
+                const __m256i g = _mm256_i32gather_epi32((const int*) g_grids.s,
+                                                         _mm256_or_si256(lo, _mm256_slli_epi32(hi, 8)), 4);
+                put_unit(U.w[j], g, rd32(blk + 74 + 4 * j));
+                U.a[j] = d * (int) (2 * ((blk[106 + j / 2] >> (4 * (j & 1))) & 15u) + 1);
+                U.b[j] = 0.0;
+            }
+            U.n = 8;
+            return;
+        }
+        case TSX_Q4_K: {
+            const float d = h2f(rd16(blk)), dmin = h2f(rd16(blk + 2));
+            const uint8_t* sc = blk + 4;
+            const __m256i low4 = _mm256_set1_epi8(15);
+            for (int j = 0; j < 8; ++j) {
+                int s, m;
+                if (j < 4) {
+                    s = sc[j] & 63;
+                    m = sc[j + 4] & 63;
+                } else {
+                    s = (sc[j + 4] & 15) | (sc[j - 4] >> 6) << 4;
+                    m = (sc[j + 4] >> 4) | (sc[j] >> 6) << 4;
+                }
+                const __m256i q = _mm256_loadu_si256((const __m256i*) (blk + 16 + 32 * (j / 2)));
+                _mm256_store_si256((__m256i*) U.w[j],
+                                   _mm256_and_si256((j & 1) ? _mm256_srli_epi16(q, 4) : q, low4));
+                U.a[j] = (double) d * s;
+                U.b[j] = (double) dmin * m;
+            }
+            U.n = 8;
+            return;
+        }
+        default: decode_block(type, blk, U); return;
+    }
+}
+// y[t] = row . act[t] for nt tokens; n_in values (whole blocks of the type).  One body, compiled twice: with the
+// AVX2 decode and dot (the CPU has AVX2), and scalar.
+#define TSX_ROW_DOT_BODY(DECODE, DOT)                                                               \
+    const int qk = type == TSX_Q8_0 ? 32 : 256;                                                     \
+    const size_t bb = tsx_type_block_bytes(type);                                                   \
+    const bool q4k = type == TSX_Q4_K;                                                              \
+    double acc[TSX_CPU_MAXT];                                                                       \
+    for (int t = 0; t < nt; ++t) acc[t] = 0.0;                                                      \
+    Units U;                                                                                        \
+    for (int64_t blk = 0; blk < n_in / qk; ++blk) {                                                 \
+        DECODE(type, row + blk * bb, U);                                                            \
+        const int64_t u0 = blk * (qk / 32);                                                         \
+        for (int j = 0; j < U.n; ++j) {                                                             \
+            const int64_t u = u0 + j;                                                               \
+            for (int t = 0; t < nt; ++t) {                                                          \
+                const int S = DOT(U.w[j], (const int8_t*) (act[t] + 36 * u + 4));                   \
+                const int M = q4k ? msum[t][u] : 0;                                                 \
+                acc[t] += d8[t][u] * (U.a[j] * S - U.b[j] * M);                                     \
+            }                                                                                       \
+        }                                                                                           \
+    }                                                                                               \
+    for (int t = 0; t < nt; ++t) y[t] = (float) acc[t];
+
+void row_dot_scalar(int type, const uint8_t* row, int64_t n_in, const uint8_t* const* act, int nt, float* y,
+                    const double* const* d8, const int* const* msum) {
+    TSX_ROW_DOT_BODY(decode_block, dot32_scalar)
+}
+__attribute__((target("avx2"))) void row_dot_avx2(int type, const uint8_t* row, int64_t n_in,
+                                                  const uint8_t* const* act, int nt, float* y,
+                                                  const double* const* d8, const int* const* msum) {
+    TSX_ROW_DOT_BODY(decode_block_avx2, dot32_avx2)
+}
+#undef TSX_ROW_DOT_BODY
+using RowDot = void (*)(int, const uint8_t*, int64_t, const uint8_t* const*, int, float*, const double* const*,
+                        const int* const*);
+const RowDot row_dot = __builtin_cpu_supports("avx2") ? row_dot_avx2 : row_dot_scalar;
 
 // per-token unit scales and code sums of nt Q8_1 rows of nu units (the caller's buffers)
 void unpack_acts(const void* const* act, int nt, int64_t nu, bool sums, double* d8, int* ms, const double** pd,

@@ -494,4 +494,63 @@ TSX_API int tsx_moe_hybrid_cpu(tsx_pool* p, const tsx_cpu_fmt* f, const uint8_t*
     return p->run(*f, jobs.data(), (int) jobs.size());
 }
 
+TSX_API int tsx_moe_hybrid_decode_layer(tsx_pool* p, const tsx_cpu_fmt* f, tsx_hybrid_layer* a, void* stream) {
+    clear_error();
+    TSX_REQUIRE(p && f && a && a->n_tok >= 1 && a->n_tok <= 8 && a->k >= 1 && a->host_blobs && a->slot_of &&
+                    a->d_slot_of && a->slots && a->x && a->logits && a->y && a->ids && a->wts && a->grp_ptr &&
+                    a->grp_start && a->n_groups && a->ent_dst && a->ent_tok && a->xq && a->scratch && a->parts &&
+                    a->h_ids && a->h_x && a->h_rows && a->h_miss && a->d_rows && a->d_miss &&
+                    (!a->shared || (a->sgate && a->sh_gate && a->sh_up && a->sh_hq && a->sh_out)),
+                "tsx_moe_hybrid_decode_layer: a null buffer, or n_tok outside 1..8");
+    const tsx_expert_layout& L = a->L;
+    const int T = a->n_tok, k = a->k, n_ent = T * k, N = (int) L.n_embd, FF = (int) L.n_ff;
+    const hipStream_t st = (hipStream_t) stream;
+    thread_local hipEvent_t routed = nullptr;
+    if (!routed && hipEventCreateWithFlags(&routed, hipEventDisableTiming) != hipSuccess) {
+        set_error("tsx_moe_hybrid_decode_layer: hipEventCreate failed");
+        return TSX_ERR_ARG;
+    }
+    int rc;
+#define TSX_TRY(call)                    \
+    if ((rc = (call)) != TSX_OK) return rc;
+#define TSX_HIP(call)                                                                           \
+    if (hipError_t e = (call); e != hipSuccess) {                                               \
+        set_error("tsx_moe_hybrid_decode_layer: %s: %s", #call, hipGetErrorString(e));          \
+        return (int) e;                                                                         \
+    }
+    // the GPU half: routing and its round trip first, then the resident experts and the shared expert
+    TSX_TRY(tsx_moe_router_topk(a->logits, a->ids, a->wts, a->n_expert, k, T, stream));
+    TSX_HIP(hipMemcpyAsync(a->h_ids, a->ids, sizeof(int32_t) * (size_t) n_ent, hipMemcpyDeviceToHost, st));
+    TSX_HIP(hipMemcpyAsync(a->h_x, a->x, sizeof(float) * (size_t) T * N, hipMemcpyDeviceToHost, st));
+    TSX_HIP(hipEventRecord(routed, st));
+    TSX_TRY(tsx_moe_group_resident(a->ids, n_ent, k, a->n_expert, a->d_slot_of, a->slots, a->stride, a->grp_ptr,
+                                   a->grp_start, a->n_groups, a->ent_dst, a->ent_tok, stream));
+    TSX_TRY(tsx_moe_quantize_q8_1(a->x, T, N, a->xq, stream));
+    const int64_t cap = std::min(n_ent, a->n_expert);
+    TSX_TRY(tsx_moe_expert_grouped(&L, a->grp_ptr, a->grp_start, a->n_groups, a->ent_dst, a->ent_tok, cap, n_ent,
+                                   a->xq, a->scratch, a->parts, stream, 0));
+    if (a->shared) {
+        const uint8_t* sh = (const uint8_t*) a->shared;
+        TSX_TRY(tsx_moe_mmvq(L.gu_type, sh, a->xq, a->sh_gate, N, FF, T, stream));
+        TSX_TRY(tsx_moe_mmvq(L.gu_type, sh + L.up_off, a->xq, a->sh_up, N, FF, T, stream));
+        TSX_TRY(tsx_moe_swiglu_quantize_q8_1(a->sh_gate, a->sh_up, (int64_t) T * FF, a->sh_hq, stream));
+        TSX_TRY(tsx_moe_mmvq(L.d_type, sh + L.down_off, a->sh_hq, a->sh_out, FF, N, T, stream));
+    }
+    // the CPU half while the GPU runs: the misses on the pool, then their rows up and merged before the combine
+    TSX_HIP(hipEventSynchronize(routed));
+    int32_t nm = 0;
+    TSX_TRY(tsx_moe_hybrid_cpu(p, f, a->host_blobs, a->stride, a->slot_of, a->n_expert, k, T, a->h_ids, a->h_x,
+                               a->h_rows, a->h_miss, &nm));
+    a->n_miss = nm;
+    if (nm > 0) {
+        TSX_HIP(hipMemcpyAsync(a->d_rows, a->h_rows, sizeof(float) * (size_t) nm * N, hipMemcpyHostToDevice, st));
+        TSX_HIP(hipMemcpyAsync(a->d_miss, a->h_miss, sizeof(int32_t) * (size_t) n_ent, hipMemcpyHostToDevice, st));
+        TSX_TRY(tsx_moe_merge_rows(a->parts, a->d_rows, a->d_miss, n_ent, N, stream));
+    }
+    return tsx_moe_combine(a->y, a->parts, nullptr, a->wts, k, a->shared ? a->sh_out : nullptr, a->sgate,
+                           a->sg_stride, N, T, stream);
+#undef TSX_TRY
+#undef TSX_HIP
+}
+
 }  // extern "C"

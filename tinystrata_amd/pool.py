@@ -15,7 +15,7 @@ import numpy as np
 import torch
 
 from . import ops
-from ._lib import CPU_MAXT, CpuFmt, CpuJob, check, lib
+from ._lib import CPU_MAXT, CpuFmt, CpuJob, HybridLayerArgs, check, lib
 from .moe import MoEWeights
 
 
@@ -198,34 +198,28 @@ class HybridMoELayer:
         self.h_miss = torch.empty(n_ent, dtype=i32, pin_memory=True)
         self.d_rows = torch.empty((n_ent, self.N), dtype=f32, device=dev)
         self.d_miss = torch.empty(n_ent, dtype=i32, device=dev)
-        self.routed = torch.cuda.Event()
         self.n_miss = 0
 
-    def __call__(self, x: torch.Tensor, logits: torch.Tensor, sgate: torch.Tensor | None, y: torch.Tensor) -> None:
-        """y += MoE(x) as MoELayer does, with the non-resident experts computed on the CPU pool."""
-        W, L, k = self.W, self.W.L, self.k
-        ops.native_router_topk(logits, k, self.ids, self.wts)
-        self.h_ids.copy_(self.ids, non_blocking=True)
-        self.h_x.copy_(x, non_blocking=True)
-        self.routed.record()
-        gp, gs, ng, ed, et = ops.group_resident(self.ids, k, self.n_expert, self.d_slot_of, self.slots.data_ptr(),
-                                                self.stride, self.grp)
-        ops.quantize_q8_1_rows(x, self.xq)
-        ops.native_expert_grouped(L, gp, gs, ng, ed, et, self.cap_groups, self.n_ent, self.xq, self.scratch,
-                                  self.parts)
+        A = HybridLayerArgs()
+        A.L = L
+        A.n_expert, A.k, A.n_tok, A.sg_stride = self.n_expert, k, n_tok, 1
+        A.host_blobs, A.stride, A.slot_of = self.host_blobs.ctypes.data, self.stride, self.slot_of.ctypes.data
+        A.d_slot_of, A.slots = self.d_slot_of.data_ptr(), self.slots.data_ptr()
+        A.shared = W.shared.data_ptr() if W.shared is not None else None
+        for name in ("ids", "wts", "xq", "scratch", "parts", "h_ids", "h_x", "h_rows", "h_miss", "d_rows", "d_miss"):
+            setattr(A, name, getattr(self, name).data_ptr())
+        A.grp_ptr, A.grp_start, A.n_groups, A.ent_dst, A.ent_tok = (t.data_ptr() for t in self.grp)
         if W.shared is not None:
-            sh = W.shared
-            ops.iq_mmvq(L.gu_type, sh, self.xq, self.N, self.FF, self.n_tok, y=self.sg)
-            ops.iq_mmvq(L.gu_type, sh[L.up_off:], self.xq, self.N, self.FF, self.n_tok, y=self.su)
-            ops.native_swiglu_quantize_q8_1(self.sg, self.su, self.shq)
-            ops.iq_mmvq(L.d_type, sh[L.down_off:], self.shq, self.FF, self.N, self.n_tok, y=self.sh)
-        # the CPU half while the GPU runs the resident experts
-        self.routed.synchronize()
-        self.n_miss = hybrid_cpu(self.pool, self.f, self.host_blobs, self.stride, self.slot_of, k,
-                                 self.h_ids.numpy(), self.h_x.numpy(), self.h_rows.numpy(), self.h_miss.numpy())
-        if self.n_miss:
-            self.d_rows[: self.n_miss].copy_(self.h_rows[: self.n_miss], non_blocking=True)
-            self.d_miss.copy_(self.h_miss, non_blocking=True)
-            ops.merge_rows(self.parts, self.d_rows, self.d_miss)
-        ops.moe_combine(y, self.parts, self.wts, k, shared=self.sh, sgate=sgate)
-        # the pinned buffers are reused by the next call: its copies wait for this call's uploads on the stream
+            A.sh_gate, A.sh_up, A.sh_hq, A.sh_out = (t.data_ptr() for t in (self.sg, self.su, self.shq, self.sh))
+        self.args = A
+
+    def __call__(self, x: torch.Tensor, logits: torch.Tensor, sgate: torch.Tensor | None, y: torch.Tensor) -> None:
+        """y += MoE(x) as MoELayer does, with the non-resident experts computed on the CPU pool: one library call
+        (tsx_moe_hybrid_decode_layer) enqueues the GPU half, runs the CPU half while the GPU works, and enqueues the
+        merge and the combine."""
+        A = self.args
+        A.x, A.logits, A.y = x.data_ptr(), logits.data_ptr(), y.data_ptr()
+        A.sgate = sgate.data_ptr() if sgate is not None else None
+        check(lib().tsx_moe_hybrid_decode_layer(self.pool.handle, C.byref(self.f), C.byref(A),
+                                                torch.cuda.current_stream(y.device).cuda_stream), "hybrid layer")
+        self.n_miss = A.n_miss
