@@ -216,42 +216,50 @@ __attribute__((target("avx2"))) inline void decode_block_avx2(int type, const ui
         default: decode_block(type, blk, U); return;
     }
 }
-// y[t] = row . act[t] for nt tokens; n_in values (whole blocks of the type).  One body, compiled twice: with the
-// AVX2 decode and dot (the CPU has AVX2), and scalar.
+// y[r][t] = row r . act[t] for two rows (rows[1] may equal rows[0]) and nt tokens; n_in values (whole blocks of the
+// type).  Two rows at once keep two independent accumulation chains in flight; each row's sum runs over its units in
+// order, so the value is the one-row value.  One body, compiled twice: with the AVX2 decode and dot (the CPU has
+// AVX2), and scalar.
 #define TSX_ROW_DOT_BODY(DECODE, DOT)                                                               \
     const int qk = type == TSX_Q8_0 ? 32 : 256;                                                     \
     const size_t bb = tsx_type_block_bytes(type);                                                   \
     const bool q4k = type == TSX_Q4_K;                                                              \
-    double acc[TSX_CPU_MAXT];                                                                       \
-    for (int t = 0; t < nt; ++t) acc[t] = 0.0;                                                      \
-    Units U;                                                                                        \
+    double acc[2][TSX_CPU_MAXT];                                                                    \
+    for (int t = 0; t < nt; ++t) acc[0][t] = acc[1][t] = 0.0;                                       \
+    Units U[2];                                                                                     \
     for (int64_t blk = 0; blk < n_in / qk; ++blk) {                                                 \
-        DECODE(type, row + blk * bb, U);                                                            \
+        DECODE(type, rows[0] + blk * bb, U[0]);                                                     \
+        DECODE(type, rows[1] + blk * bb, U[1]);                                                     \
         const int64_t u0 = blk * (qk / 32);                                                         \
-        for (int j = 0; j < U.n; ++j) {                                                             \
+        for (int j = 0; j < U[0].n; ++j) {                                                          \
             const int64_t u = u0 + j;                                                               \
             for (int t = 0; t < nt; ++t) {                                                          \
-                const int S = DOT(U.w[j], (const int8_t*) (act[t] + 36 * u + 4));                   \
+                const int8_t* a8 = (const int8_t*) (act[t] + 36 * u + 4);                           \
+                const int S0 = DOT(U[0].w[j], a8), S1 = DOT(U[1].w[j], a8);                         \
                 const int M = q4k ? msum[t][u] : 0;                                                 \
-                acc[t] += d8[t][u] * (U.a[j] * S - U.b[j] * M);                                     \
+                acc[0][t] += d8[t][u] * (U[0].a[j] * S0 - U[0].b[j] * M);                           \
+                acc[1][t] += d8[t][u] * (U[1].a[j] * S1 - U[1].b[j] * M);                           \
             }                                                                                       \
         }                                                                                           \
     }                                                                                               \
-    for (int t = 0; t < nt; ++t) y[t] = (float) acc[t];
+    for (int t = 0; t < nt; ++t) {                                                                  \
+        y[0][t] = (float) acc[0][t];                                                                \
+        y[1][t] = (float) acc[1][t];                                                                \
+    }
 
-void row_dot_scalar(int type, const uint8_t* row, int64_t n_in, const uint8_t* const* act, int nt, float* y,
-                    const double* const* d8, const int* const* msum) {
+void row_dot_scalar(int type, const uint8_t* const* rows, int64_t n_in, const uint8_t* const* act, int nt,
+                    float (*y)[TSX_CPU_MAXT], const double* const* d8, const int* const* msum) {
     TSX_ROW_DOT_BODY(decode_block, dot32_scalar)
 }
-__attribute__((target("avx2"))) void row_dot_avx2(int type, const uint8_t* row, int64_t n_in,
-                                                  const uint8_t* const* act, int nt, float* y,
+__attribute__((target("avx2"))) void row_dot_avx2(int type, const uint8_t* const* rows, int64_t n_in,
+                                                  const uint8_t* const* act, int nt, float (*y)[TSX_CPU_MAXT],
                                                   const double* const* d8, const int* const* msum) {
     TSX_ROW_DOT_BODY(decode_block_avx2, dot32_avx2)
 }
 #undef TSX_ROW_DOT_BODY
-using RowDot = void (*)(int, const uint8_t*, int64_t, const uint8_t* const*, int, float*, const double* const*,
-                        const int* const*);
-const RowDot row_dot = __builtin_cpu_supports("avx2") ? row_dot_avx2 : row_dot_scalar;
+using RowDot = void (*)(int, const uint8_t* const*, int64_t, const uint8_t* const*, int, float (*)[TSX_CPU_MAXT],
+                        const double* const*, const int* const*);
+const RowDot row_dot2 = __builtin_cpu_supports("avx2") ? row_dot_avx2 : row_dot_scalar;
 
 // per-token unit scales and code sums of nt Q8_1 rows of nu units (the caller's buffers)
 void unpack_acts(const void* const* act, int nt, int64_t nu, bool sums, double* d8, int* ms, const double** pd,
@@ -323,13 +331,13 @@ int cpu_gu_rows(const tsx_cpu_fmt& f, const uint8_t* blob, const void* const* ac
     const int* pm[TSX_CPU_MAXT];
     unpack_acts(act, nt, nu, q4k, d8, ms, pd, pm);
     const uint8_t* const* a = (const uint8_t* const*) act;
-    float g[TSX_CPU_MAXT], u[TSX_CPU_MAXT];
-    for (int r = r0; r < r1; ++r) {
-        row_dot(f.gu_type, blob + (uint64_t) r * f.gu_row, N, a, nt, g, pd, pm);
-        row_dot(f.gu_type, blob + f.up_off + (uint64_t) r * f.gu_row, N, a, nt, u, pd, pm);
+    float gu[2][TSX_CPU_MAXT];
+    for (int r = r0; r < r1; ++r) {  // gate row r and up row r together
+        const uint8_t* rows[2] = {blob + (uint64_t) r * f.gu_row, blob + f.up_off + (uint64_t) r * f.gu_row};
+        row_dot2(f.gu_type, rows, N, a, nt, gu, pd, pm);
         for (int t = 0; t < nt; ++t) {
-            const float s = g[t] / (1.0f + std::exp(-g[t]));
-            ff[t][r] = s * u[t];
+            const float s = gu[0][t] / (1.0f + std::exp(-gu[0][t]));
+            ff[t][r] = s * gu[1][t];
         }
     }
     return TSX_OK;
@@ -346,10 +354,15 @@ int cpu_down_rows(const tsx_cpu_fmt& f, const uint8_t* blob, const void* const* 
     const int* pm[TSX_CPU_MAXT];
     unpack_acts(hq, nt, nu, q4k, d8, ms, pd, pm);
     const uint8_t* const* a = (const uint8_t* const*) hq;
-    float y[TSX_CPU_MAXT];
-    for (int r = r0; r < r1; ++r) {
-        row_dot(f.d_type, blob + f.down_off + (uint64_t) r * f.d_row, FF, a, nt, y, pd, pm);
-        for (int t = 0; t < nt; ++t) out[t][r] = y[t];
+    float y[2][TSX_CPU_MAXT];
+    for (int r = r0; r < r1; r += 2) {  // rows r and r + 1 together (r alone twice at an odd end)
+        const int r2 = r + 1 < r1 ? r + 1 : r;
+        const uint8_t* rows[2] = {blob + f.down_off + (uint64_t) r * f.d_row, blob + f.down_off + (uint64_t) r2 * f.d_row};
+        row_dot2(f.d_type, rows, FF, a, nt, y, pd, pm);
+        for (int t = 0; t < nt; ++t) {
+            out[t][r] = y[0][t];
+            out[t][r2] = y[1][t];
+        }
     }
     return TSX_OK;
 }
