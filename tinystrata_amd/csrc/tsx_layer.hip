@@ -24,7 +24,7 @@
 //      of the slice's group (each unit decoded once for all entries), applies SwiGLU (the product rounded on its own)
 //      and writes the slice's Q8_1 block of h per entry.  Block 0 also writes ids / wts and the tables launch B
 //      needs.
-// Launch B, grid n_embd/8, 256 threads.  Every block owns 8 output rows: it reads the tables and every entry's h in
+// Launch B, grid n_embd/8, 1024 threads.  Every block owns 8 output rows: it reads the tables and every entry's h in
 //   one round trip, loads those 8 rows of every used expert's down matrix (and the shared expert's) into LDS,
 //   dots, and combines in pick order: y += w0*p0, fmaf(wj, pj, .) ..., + sigmoid(sgate)*shared -
 //   tsx_moe_combine's arithmetic.
