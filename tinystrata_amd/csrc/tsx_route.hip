@@ -41,18 +41,44 @@ __global__ void __launch_bounds__(256) group_kernel(const int32_t* __restrict__ 
         if (grouped(x)) atomicAdd(&cnt[x], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int g = 0, pos = 0;
-        for (int x = 0; x < n_expert; ++x) {
-            off[x] = pos;
-            if (cnt[x] == 0) continue;
-            grp_ptr[g] = (uint64_t) (blobs + (uint64_t) (slot_of ? slot_of[x] : x) * stride);
-            grp_start[g] = pos;
-            pos += cnt[x];
-            ++g;
+    // groups and offsets: each thread takes two consecutive experts; exclusive scans of their entry counts and of
+    // their used flags over the block (within a wave by shuffles, then over the four waves' totals)
+    {
+        __shared__ int wsum[2][4];
+        const int t = threadIdx.x, x0 = 2 * t, lane = t & 63, wave = t >> 6;
+        const int c0 = x0 < n_expert ? cnt[x0] : 0, c1 = x0 + 1 < n_expert ? cnt[x0 + 1] : 0;
+        int s = c0 + c1, g = (c0 > 0) + (c1 > 0);
+        for (int o = 1; o < 64; o <<= 1) {
+            const int ps = __shfl_up(s, o, 64), pg = __shfl_up(g, o, 64);
+            if (lane >= o) {
+                s += ps;
+                g += pg;
+            }
         }
-        grp_start[g] = pos;
-        *n_groups = g;
+        if (lane == 63) {
+            wsum[0][wave] = s;
+            wsum[1][wave] = g;
+        }
+        __syncthreads();
+        for (int w = 0; w < wave; ++w) {
+            s += wsum[0][w];
+            g += wsum[1][w];
+        }
+        const int pos = s - c0 - c1, gi = g - (c0 > 0) - (c1 > 0);  // exclusive
+        if (x0 < n_expert) off[x0] = pos;
+        if (x0 + 1 < n_expert) off[x0 + 1] = pos + c0;
+        if (c0 > 0) {
+            grp_ptr[gi] = (uint64_t) (blobs + (uint64_t) (slot_of ? slot_of[x0] : x0) * stride);
+            grp_start[gi] = pos;
+        }
+        if (c1 > 0) {
+            grp_ptr[gi + (c0 > 0)] = (uint64_t) (blobs + (uint64_t) (slot_of ? slot_of[x0 + 1] : x0 + 1) * stride);
+            grp_start[gi + (c0 > 0)] = pos + c0;
+        }
+        if (t == (int) blockDim.x - 1) {  // inclusive totals of the last thread
+            grp_start[g] = s;
+            *n_groups = g;
+        }
     }
     __syncthreads();
     // the entries in entry order: wave-sized chunks, ranks from ballots, chunks committed in order
