@@ -75,7 +75,8 @@ TSX_API int tsx_pool_workers(const tsx_pool* p);
 TSX_API int tsx_pool_host_works(const tsx_pool* p);
 /* Evaluates n jobs (any number; batches of TSX_POOL_MAX_SPLIT): gate/up rows, SwiGLU + Q8_1 of h, down rows, as
  * dependent row tasks per expert when several experts and threads take part, else as three phases.  Returns when
- * every job's outputs are written.  One caller at a time per pool.
+ * every job's outputs are written.  One caller at a time per pool.  After TSX_ERR_STALLED, workers may still be
+ * running the batch: the jobs and their buffers must stay valid until tsx_pool_destroy has returned.
  * Replaces ExpertPool::run_split_multi_native (pool.hpp:139; src/kernels/cpu/pool.cpp:773-817). */
 TSX_API int tsx_pool_run(tsx_pool* p, const tsx_cpu_fmt* f, const tsx_cpu_job* jobs, int n);
 /* Accumulated milliseconds: [0] waiting for parked workers, [1] draining, [2] phases gate/up, [3] quantize h,

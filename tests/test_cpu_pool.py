@@ -154,3 +154,24 @@ def test_hybrid_cpu_half(T):
     assert np.isnan(rows[nm:]).all()  # nothing past the misses
     with ExpertPool(1, pin=False) as p, pytest.raises(_lib.TsxError):
         hybrid_cpu(p, f, blobs, blobs.shape[1], slot_of, k, np.full((T, k), E, np.int32), x, rows, miss)
+
+
+def test_pool_stall_is_an_error_not_a_hang():
+    """A run that makes no progress for the stall limit returns TSX_ERR_STALLED (the reference aborts the engine
+    there, src/kernels/cpu/pool.cpp:655-677), and the pool takes no more work.  The stall is forced from the host:
+    a 1 ms limit, one worker and the host not draining, against jobs that take far longer."""
+    N, FF = 2048, 512
+    f = cpu_fmt(IQ3_XXS, IQ3_S, N, FF)
+    blobs = experts(IQ3_XXS, IQ3_S, N, FF, 2, seed=6)
+    act = cpu_quant_act(f, np.ones(N, np.float32))
+    p = ExpertPool(1, pin=False, host_works=False, tasks=1)
+    p.set_stall_ms(1)
+    jobs = [(blobs[j % 2], [act] * 8, [np.zeros(N, np.float32) for _ in range(8)]) for j in range(1)]
+    with pytest.raises(_lib.TsxError) as e:
+        for _ in range(50):  # a single slow task: the host sees no completion for 1 ms
+            p.run(f, jobs)
+    assert e.value.rc == _lib.TSX_ERR_STALLED
+    with pytest.raises(_lib.TsxError) as e:
+        p.run(f, jobs)
+    assert e.value.rc == _lib.TSX_ERR_STALLED
+    p.close()  # joins the worker once its task ends

@@ -105,6 +105,7 @@ class ExpertPool:
                 assert outs[t].dtype == np.float32 and outs[t].flags.c_contiguous
                 arr[i].act[t] = _ptr(acts[t])
                 arr[i].out[t] = _ptr(outs[t])
+        self._last = (arr, jobs)  # workers of a stalled run may still read them: kept until the next run or close()
         check(lib().tsx_pool_run(self._h, C.byref(f), arr, len(jobs)), "pool run")
 
     def stats(self) -> dict:
@@ -116,8 +117,9 @@ class ExpertPool:
 
     def close(self) -> None:
         if self._h:
-            lib().tsx_pool_destroy(self._h)
+            lib().tsx_pool_destroy(self._h)  # joins the workers
             self._h = C.c_void_p()
+        self._last = None
 
     def __enter__(self) -> "ExpertPool":
         return self
