@@ -505,7 +505,14 @@ TSX_API int tsx_moe_hybrid_decode_layer(tsx_pool* p, const tsx_cpu_fmt* f, tsx_h
     const tsx_expert_layout& L = a->L;
     const int T = a->n_tok, k = a->k, n_ent = T * k, N = (int) L.n_embd, FF = (int) L.n_ff;
     const hipStream_t st = (hipStream_t) stream;
-    thread_local hipEvent_t routed = nullptr;
+    // one event per calling thread and device (an event records only on a stream of its own device)
+    thread_local hipEvent_t events[64] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
+        set_error("tsx_moe_hybrid_decode_layer: no current device (or more than 64)");
+        return TSX_ERR_ARG;
+    }
+    hipEvent_t& routed = events[device];
     if (!routed && hipEventCreateWithFlags(&routed, hipEventDisableTiming) != hipSuccess) {
         set_error("tsx_moe_hybrid_decode_layer: hipEventCreate failed");
         return TSX_ERR_ARG;
