@@ -129,7 +129,7 @@ def test_pool_default_size_and_pinning():
             assert np.array_equal(np.stack(outs), w)
 
 
-@pytest.mark.parametrize("T", [1, 4])
+@pytest.mark.parametrize("T", [1, 4, 12])  # 12 tokens: experts with more than 8 misses take two jobs
 def test_hybrid_cpu_half(T):
     N, FF, E, k = 512, 256, 24, 8
     f = cpu_fmt(IQ3_XXS, IQ3_S, N, FF)

@@ -11,7 +11,7 @@ import torch
 
 import oracle as O
 from tinystrata_amd import moe, ops
-from tinystrata_amd._lib import IQ3_S, IQ3_XXS, Q8_0
+from tinystrata_amd._lib import IQ3_S, IQ3_XXS, Q4_K, Q8_0
 from tinystrata_amd.pool import ExpertPool, HybridMoELayer
 
 from gpu_util import dev, host, pool, rel_l2
@@ -20,7 +20,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("gu,d,T,every", [(IQ3_XXS, IQ3_S, 1, 2), (IQ3_XXS, IQ3_S, 4, 3), (IQ3_XXS, IQ3_S, 4, 0),
-                                          (IQ3_XXS, IQ3_S, 1, 1), (Q8_0, Q8_0, 2, 2)])
+                                          (IQ3_XXS, IQ3_S, 1, 1), (Q8_0, Q8_0, 2, 2), (Q4_K, Q4_K, 8, 2)])
 def test_hybrid_layer(gu, d, T, every):
     N, FF, E, k, distinct = 2048, 512, 64, 8, 6
     print(f"hybrid layer types {gu}/{d} T={T} resident every {every}", flush=True)
