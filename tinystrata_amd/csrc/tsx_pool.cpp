@@ -97,8 +97,8 @@ struct tsx_pool {
     int n_ = 0;
     bool host_works_ = true;
     int tasks_ = 0;
-    std::chrono::microseconds spin_{20000};
-    std::chrono::milliseconds stall_{60000};
+    std::atomic<int64_t> spin_us_{20000};   // set between runs, read by parked workers
+    std::atomic<int64_t> stall_ms_{60000};
 
     alignas(64) std::atomic<uint64_t> head_{0};
     alignas(64) std::atomic<uint32_t> done_{0};
@@ -170,7 +170,7 @@ struct tsx_pool {
                 cpu_relax();
                 if ((++spins & 63u) != 0) continue;
                 const auto now = Clock::now();
-                if (now - parked_at < spin_) {
+                if (now - parked_at < std::chrono::microseconds(spin_us_.load(std::memory_order_relaxed))) {
                     if (now >= yield_at) {
                         std::this_thread::yield();
                         yield_at = now + std::chrono::microseconds(50);
@@ -211,7 +211,7 @@ struct tsx_pool {
             if (p != last) {
                 last = p;
                 t0 = now;
-            } else if (now - t0 > stall_) {
+            } else if (now - t0 > std::chrono::milliseconds(stall_ms_.load(std::memory_order_relaxed))) {
                 tsx::set_error("tsx_pool: stalled %s (%u of %d jobs done, %u of %d workers parked)", what,
                                done_.load(), ntasks_, parked_.load(), n_);
                 failed_.store(true);
@@ -437,14 +437,14 @@ TSX_API int tsx_pool_stats(const tsx_pool* p, double* ms6, int64_t* bytes) {
 TSX_API int tsx_pool_set_spin_us(tsx_pool* p, int64_t us) {
     clear_error();
     TSX_REQUIRE(p && us >= 0, "tsx_pool_set_spin_us: pool, us >= 0");
-    p->spin_ = std::chrono::microseconds(us);
+    p->spin_us_.store(us);
     return TSX_OK;
 }
 
 TSX_API int tsx_pool_set_stall_ms(tsx_pool* p, int64_t ms) {
     clear_error();
     TSX_REQUIRE(p && ms > 0, "tsx_pool_set_stall_ms: pool, ms > 0");
-    p->stall_ = std::chrono::milliseconds(ms);
+    p->stall_ms_.store(ms);
     return TSX_OK;
 }
 
