@@ -83,6 +83,11 @@ TSX_API int tsx_pool_run(tsx_pool* p, const tsx_cpu_fmt* f, const tsx_cpu_job* j
  * [4] down, [5] fused batches; and *bytes = expert blob bytes evaluated.  Replaces ExpertPool::phase_ms and the
  * ms_multi_* counters (pool.hpp:140-143,160-167). */
 TSX_API int tsx_pool_stats(const tsx_pool* p, double* ms6, int64_t* bytes);
+/* The pool's state as one line of text into buf (n bytes, truncated): the epoch, the head word's epoch / jobs /
+ * next index, done, parked, sleepers, and each worker's state (parked, sleeping, between batches, or the job it
+ * runs).  Safe to call from any thread at any time.  Replaces ExpertPool::diag (pool.hpp:118-119,
+ * src/kernels/cpu/pool.cpp:457-476). */
+TSX_API int tsx_pool_diag(const tsx_pool* p, char* buf, size_t n);
 /* How long a parked worker spins before it sleeps, in microseconds (default 20000): a test knob, as the reference's
  * STRATA_POOL_SPIN_US (pool.hpp:180-181).  Only between runs. */
 TSX_API int tsx_pool_set_spin_us(tsx_pool* p, int64_t us);

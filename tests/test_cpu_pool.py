@@ -100,6 +100,9 @@ def test_pool_equals_serial(workers, host_works, tasks):
                 assert np.array_equal(np.stack(outs).view(np.uint32), w.view(np.uint32))
         st = p.stats()
         assert st["bytes"] == (1 + 2 + 13 + 100) * f.bytes and st["drain"] > 0
+        d = p.diag()
+        assert f"parked {workers}/{workers}" in d and "FAILED" not in d and d.count("parked") + d.count(
+            "sleeping") == workers + 1, d
 
 
 def test_pool_sleeping_workers():

@@ -218,6 +218,7 @@ POOL_SIGNATURES = {
     "tsx_pool_host_works": (I32, [P]),
     "tsx_pool_run": (I32, [P, C.POINTER(CpuFmt), C.POINTER(CpuJob), I32]),
     "tsx_pool_stats": (I32, [P, C.POINTER(C.c_double), C.POINTER(I64)]),
+    "tsx_pool_diag": (I32, [P, P, SZ]),
     "tsx_pool_set_spin_us": (I32, [P, I64]),
     "tsx_pool_set_stall_ms": (I32, [P, I64]),
     "tsx_moe_hybrid_cpu": (I32, [P, C.POINTER(CpuFmt), P, U64, P, I32, I32, I32, P, P, P, P, P]),

@@ -110,6 +110,9 @@ struct tsx_pool {
     std::mutex mu_;
     std::condition_variable cv_;
     std::vector<std::thread> threads_;
+    // each worker's state for tsx_pool_diag: parked, sleeping, between batches, or the job it runs
+    static constexpr int32_t kParked = -1, kSleeping = -2, kBetween = -3;
+    std::unique_ptr<std::atomic<int32_t>[]> wstate_;
 
     // the current batch: written by the host before it publishes, read by the workers after their acquire
     Mode mode_ = kNone;
@@ -158,8 +161,9 @@ struct tsx_pool {
                 return (int) i;
         }
     }
-    void worker() {
+    void worker(int id) {
         uint32_t seen = 0;
+        wstate_[id].store(kParked, std::memory_order_relaxed);
         parked_.fetch_add(1, std::memory_order_acq_rel);  // parked from the start: the first run waits for that
         for (;;) {
             const auto parked_at = Clock::now();
@@ -178,21 +182,26 @@ struct tsx_pool {
                     continue;
                 }
                 std::unique_lock<std::mutex> lk(mu_);
+                wstate_[id].store(kSleeping, std::memory_order_relaxed);
                 sleepers_.fetch_add(1, std::memory_order_seq_cst);
                 cv_.wait(lk, [&] {
                     return epoch_.load(std::memory_order_seq_cst) != seen || stop_.load(std::memory_order_relaxed);
                 });
                 sleepers_.fetch_sub(1, std::memory_order_relaxed);
+                wstate_[id].store(kParked, std::memory_order_relaxed);
             }
             if (stop_.load(std::memory_order_acquire)) return;
             seen = epoch_.load(std::memory_order_acquire);
             parked_.fetch_sub(1, std::memory_order_acq_rel);
-            drain(seen);
+            wstate_[id].store(kBetween, std::memory_order_relaxed);
+            drain(seen, id);
+            wstate_[id].store(kParked, std::memory_order_relaxed);
             parked_.fetch_add(1, std::memory_order_acq_rel);
         }
     }
-    void drain(uint32_t epoch) {
+    void drain(uint32_t epoch, int id = -1) {
         for (int i; (i = claim(epoch)) >= 0;) {
+            if (id >= 0) wstate_[id].store(i, std::memory_order_relaxed);
             run_task(i);
             done_.fetch_add(1, std::memory_order_release);
         }
@@ -380,11 +389,13 @@ TSX_API int tsx_pool_create(int n_workers, int pin, int host_works, int tasks, t
     if (n_workers <= 0) n_workers = std::max(1, (int) cores.size() - 1);
     auto p = std::make_unique<tsx_pool>();
     p->n_ = n_workers;
+    p->wstate_.reset(new std::atomic<int32_t>[(size_t) n_workers]);
+    for (int i = 0; i < n_workers; ++i) p->wstate_[i].store(tsx_pool::kParked);
     p->host_works_ = host_works != 0;
     p->tasks_ = tasks;
     try {
         for (int i = 0; i < n_workers; ++i) {
-            p->threads_.emplace_back([q = p.get()] { q->worker(); });
+            p->threads_.emplace_back([q = p.get(), i] { q->worker(i); });
             // worker i on physical core i + 1 (the first is the host thread's), while there are cores
             if (pin && i + 1 < (int) cores.size()) {
                 cpu_set_t set;
@@ -431,6 +442,24 @@ TSX_API int tsx_pool_stats(const tsx_pool* p, double* ms6, int64_t* bytes) {
     const double v[6] = {p->ms_park_, p->ms_drain_, p->ms_gu_, p->ms_q_, p->ms_down_, p->ms_fused_};
     for (int i = 0; i < 6; ++i) ms6[i] = v[i];
     if (bytes) *bytes = p->bytes_;
+    return TSX_OK;
+}
+
+TSX_API int tsx_pool_diag(const tsx_pool* p, char* buf, size_t n) {
+    clear_error();
+    TSX_REQUIRE(p && buf && n > 0, "tsx_pool_diag: pool and a buffer");
+    const uint64_t h = p->head_.load();
+    int w = std::snprintf(buf, n, "epoch %u head epoch %u jobs %u next %u done %u parked %u/%d sleepers %u%s; workers:",
+                          p->epoch_.load(), (uint32_t) (h >> 32), (uint32_t) (h >> 16) & 0xFFFFu,
+                          (uint32_t) h & 0xFFFFu, p->done_.load(), p->parked_.load(), p->n_, p->sleepers_.load(),
+                          p->failed_.load() ? " FAILED" : "");
+    for (int i = 0; i < p->n_ && w > 0 && (size_t) w < n; ++i) {
+        const int32_t st = p->wstate_[i].load();
+        const char* name = st == tsx_pool::kParked ? "parked" : st == tsx_pool::kSleeping ? "sleeping"
+                           : st == tsx_pool::kBetween ? "between" : nullptr;
+        w += name ? std::snprintf(buf + w, n - (size_t) w, " %s", name)
+                  : std::snprintf(buf + w, n - (size_t) w, " job %d", st);
+    }
     return TSX_OK;
 }
 

@@ -87,6 +87,12 @@ class ExpertPool:
     def host_works(self) -> bool:
         return bool(lib().tsx_pool_host_works(self._h))
 
+    def diag(self) -> str:
+        """One line: the batch counters and every worker's state (reference ExpertPool::diag)."""
+        buf = C.create_string_buffer(4096)
+        check(lib().tsx_pool_diag(self._h, buf, len(buf)), "pool diag")
+        return buf.value.decode()
+
     def set_spin_us(self, us: int) -> None:
         check(lib().tsx_pool_set_spin_us(self._h, us), "pool set_spin_us")
 
