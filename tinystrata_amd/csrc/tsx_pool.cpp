@@ -112,7 +112,10 @@ struct tsx_pool {
     std::vector<std::thread> threads_;
     // each worker's state for tsx_pool_diag: parked, sleeping, between batches, or the job it runs
     static constexpr int32_t kParked = -1, kSleeping = -2, kBetween = -3;
-    std::unique_ptr<std::atomic<int32_t>[]> wstate_;
+    struct alignas(64) WState {  // a line each: a worker's stores never contend with another's
+        std::atomic<int32_t> v{kParked};
+    };
+    std::unique_ptr<WState[]> wstate_;
 
     // the current batch: written by the host before it publishes, read by the workers after their acquire
     Mode mode_ = kNone;
@@ -163,7 +166,7 @@ struct tsx_pool {
     }
     void worker(int id) {
         uint32_t seen = 0;
-        wstate_[id].store(kParked, std::memory_order_relaxed);
+        wstate_[id].v.store(kParked, std::memory_order_relaxed);
         parked_.fetch_add(1, std::memory_order_acq_rel);  // parked from the start: the first run waits for that
         for (;;) {
             const auto parked_at = Clock::now();
@@ -182,26 +185,26 @@ struct tsx_pool {
                     continue;
                 }
                 std::unique_lock<std::mutex> lk(mu_);
-                wstate_[id].store(kSleeping, std::memory_order_relaxed);
+                wstate_[id].v.store(kSleeping, std::memory_order_relaxed);
                 sleepers_.fetch_add(1, std::memory_order_seq_cst);
                 cv_.wait(lk, [&] {
                     return epoch_.load(std::memory_order_seq_cst) != seen || stop_.load(std::memory_order_relaxed);
                 });
                 sleepers_.fetch_sub(1, std::memory_order_relaxed);
-                wstate_[id].store(kParked, std::memory_order_relaxed);
+                wstate_[id].v.store(kParked, std::memory_order_relaxed);
             }
             if (stop_.load(std::memory_order_acquire)) return;
             seen = epoch_.load(std::memory_order_acquire);
             parked_.fetch_sub(1, std::memory_order_acq_rel);
-            wstate_[id].store(kBetween, std::memory_order_relaxed);
+            wstate_[id].v.store(kBetween, std::memory_order_relaxed);
             drain(seen, id);
-            wstate_[id].store(kParked, std::memory_order_relaxed);
+            wstate_[id].v.store(kParked, std::memory_order_relaxed);
             parked_.fetch_add(1, std::memory_order_acq_rel);
         }
     }
     void drain(uint32_t epoch, int id = -1) {
         for (int i; (i = claim(epoch)) >= 0;) {
-            if (id >= 0) wstate_[id].store(i, std::memory_order_relaxed);
+            if (id >= 0) wstate_[id].v.store(i, std::memory_order_relaxed);
             run_task(i);
             done_.fetch_add(1, std::memory_order_release);
         }
@@ -389,8 +392,7 @@ TSX_API int tsx_pool_create(int n_workers, int pin, int host_works, int tasks, t
     if (n_workers <= 0) n_workers = std::max(1, (int) cores.size() - 1);
     auto p = std::make_unique<tsx_pool>();
     p->n_ = n_workers;
-    p->wstate_.reset(new std::atomic<int32_t>[(size_t) n_workers]);
-    for (int i = 0; i < n_workers; ++i) p->wstate_[i].store(tsx_pool::kParked);
+    p->wstate_.reset(new tsx_pool::WState[(size_t) n_workers]);
     p->host_works_ = host_works != 0;
     p->tasks_ = tasks;
     try {
@@ -454,7 +456,7 @@ TSX_API int tsx_pool_diag(const tsx_pool* p, char* buf, size_t n) {
                           (uint32_t) h & 0xFFFFu, p->done_.load(), p->parked_.load(), p->n_, p->sleepers_.load(),
                           p->failed_.load() ? " FAILED" : "");
     for (int i = 0; i < p->n_ && w > 0 && (size_t) w < n; ++i) {
-        const int32_t st = p->wstate_[i].load();
+        const int32_t st = p->wstate_[i].v.load();
         const char* name = st == tsx_pool::kParked ? "parked" : st == tsx_pool::kSleeping ? "sleeping"
                            : st == tsx_pool::kBetween ? "between" : nullptr;
         w += name ? std::snprintf(buf + w, n - (size_t) w, " %s", name)
