@@ -6,6 +6,8 @@ sub-block sums and the same double accumulation order), the Q8_1 bytes identical
 the same bits as the serial rows (the reference's own pool test proves pool == serial,
 tests/native-expert-pool.cpp); the hybrid CPU half numbers the misses in entry order (compact rows, reference
 moe_hybrid_cpu, src/qwen35/q36_engine.cu:3140-3160)."""
+import time
+
 import numpy as np
 import pytest
 
@@ -99,10 +101,17 @@ def test_pool_equals_serial(workers, host_works, tasks):
             for (_, _, outs), w in zip(jobs, want):
                 assert np.array_equal(np.stack(outs).view(np.uint32), w.view(np.uint32))
         st = p.stats()
-        assert st["bytes"] == (1 + 2 + 13 + 100) * f.bytes and st["drain"] > 0
+        assert st["bytes"] == (1 + 2 + 13 + 100) * f.bytes and st["drain"] > 0 and st["gate_up"] > 0
+        assert st["down"] > 0 and st["quant_h"] > 0
+        # run() returns once every chunk is finished; workers still scanning the batch leave it right after
         d = p.diag()
-        assert f"parked {workers}/{workers}" in d and "FAILED" not in d and d.count("parked") + d.count(
-            "sleeping") == workers + 1, d
+        for _ in range(2000):
+            if f"idle {workers}/{workers}" in d and "attached 0|0" in d:
+                break
+            time.sleep(0.001)
+            d = p.diag()
+        assert f"idle {workers}/{workers}" in d and "attached 0|0" in d and "FAILED" not in d, d
+        assert "0 unclaimed" in d and d.count("idle") + d.count("sleeping") == workers + 1, d
 
 
 def test_pool_sleeping_workers():
@@ -178,3 +187,28 @@ def test_pool_stall_is_an_error_not_a_hang():
         p.run(f, jobs)
     assert e.value.rc == _lib.TSX_ERR_STALLED
     p.close()  # joins the worker once its task ends
+
+
+def test_hybrid_cpu_stall_then_destroy():
+    """A stall inside tsx_moe_hybrid_cpu: the call returns TSX_ERR_STALLED, the next call is refused before it touches
+    the pool's token rows (which the stalled batch's worker may still read), and destroying the pool joins that worker
+    while the job table it reads is still the pool's own copy."""
+    N, FF, E, k, T = 2048, 512, 4, 4, 8
+    f = cpu_fmt(Q8_0, Q8_0, N, FF)
+    blobs = experts(Q8_0, Q8_0, N, FF, E, seed=7)
+    ids = (np.arange(T * k) % E).reshape(T, k).astype(np.int32)
+    x = np.random.default_rng(1).normal(0, 1, (T, N)).astype(np.float32)
+    slot_of = np.full(E, -1, np.int32)
+    rows = np.zeros((T * k, N), np.float32)
+    miss = np.zeros(T * k, np.int32)
+    p = ExpertPool(1, pin=False, host_works=False, tasks=1)
+    p.set_stall_ms(1)
+    with pytest.raises(_lib.TsxError) as e:
+        for _ in range(50):
+            hybrid_cpu(p, f, blobs, blobs.shape[1], slot_of, k, ids, x, rows, miss)
+    assert e.value.rc == _lib.TSX_ERR_STALLED
+    with pytest.raises(_lib.TsxError) as e:
+        hybrid_cpu(p, f, blobs, blobs.shape[1], slot_of, k, ids, x, rows, miss)
+    assert e.value.rc == _lib.TSX_ERR_STALLED and "takes no more work" in str(e.value)
+    assert "FAILED" in p.diag()
+    p.close()

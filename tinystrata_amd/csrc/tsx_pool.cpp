@@ -1,34 +1,46 @@
 // tsx_pool.cpp - the CPU expert pool of the hybrid split: worker threads that evaluate the routed experts without a
-// slot in HBM, in row tasks, while the GPU runs the resident ones.
+// slot in HBM while the GPU runs the resident ones.
 //
 // Reference: strata::kernels::cpu::ExpertPool (include/strata/kernels/cpu/pool.hpp:111-260,
 // src/kernels/cpu/pool.cpp:457-817) and the engine's CPU half of a hybrid layer (moe_hybrid_cpu,
-// src/qwen35/q36_engine.cu:3090-3209).
+// src/qwen35/q36_engine.cu:3090-3209).  What must hold is the reference's contract (pool.hpp:1-15): a worker never
+// runs work of a batch other than the one it joined, never runs a piece twice, never counts into a batch the host
+// has moved past, and no wait is unbounded.  This file meets it with a design of its own:
 //
-// The completion protocol is the reference's (pool.hpp:1-15), in code of this library's own:
-//   * A batch is published by writing its description, resetting `done`, storing `head` = epoch << 32 |
-//     njobs << 16 | 0 and bumping `epoch` (seq_cst, so a worker going to sleep and the host publishing cannot both
-//     miss each other: the worker adds itself to `sleepers` and then reads `epoch`, the host bumps `epoch` and then
-//     reads `sleepers`).
-//   * A claim is a CAS on `head` that succeeds only for the epoch the worker woke for, so a worker that wakes late
-//     can never take a job of a later batch, run a job twice, or add to a `done` that was already reset.
-//   * The host waits for `done == njobs` and then for every worker to be parked again before it writes the next
-//     batch.  Every wait is bounded (`stall`): a pool that sees no progress for that long marks itself failed and
-//     returns TSX_ERR_STALLED instead of spinning forever.
-//   * A parked worker spins with a pause instruction, yields every 50 us, and sleeps on a condition variable after
-//     `spin` (20 ms by default), so an idle engine does not hold every core busy.
-// Each shared atomic sits on its own cache line.  The row decomposition changes no result: every output row is one
-// tsx_cpu_gu_rows / tsx_cpu_down_rows row, whichever thread computes it.
+//   * Two batch slots used in turn.  The host writes a slot's description - its own copy of the format and the job
+//     table, fresh counters - and then publishes the batch by storing its sequence number in `current_`.
+//   * Joining: a worker adds itself to the slot's `attached` count and only then re-reads `current_`.  If the batch
+//     is no longer current it leaves, having touched nothing but `attached`.  The host rewrites a slot only after
+//     `attached` has fallen to zero, so a worker that joined a batch sees that batch's description for as long as it
+//     stays (both sides use sequentially consistent operations, so either the worker sees the newer batch number or
+//     the host sees the worker attached).
+//   * Work is claimed per expert and no piece of work ever waits inside: every expert has a cursor over its gate/up
+//     row chunks and one over its down row chunks.  The thread that completes an expert's last gate/up chunk
+//     quantizes h and opens the expert's down chunks.  A thread that finds nothing open on one expert moves on to
+//     the next; it spins only when nothing at all is open (every remaining chunk waits for an h being made).
+//   * The host returns once the slot's `finished` count reaches the batch's chunk count (release/acquire: every
+//     output row is then visible); it waits for `attached` only when it needs the slot again, two batches later.
+//   * Idle workers spin with a pause, yield now and then, and after `spin_us_` sleep on a futex word the host bumps on
+//     every publish; a sleeper count spares the system call while nobody sleeps.
+//   * Every host wait is bounded by `stall_ms_`: a batch that makes no progress for that long marks the pool failed,
+//     the call returns TSX_ERR_STALLED and the pool takes no further work.  The job table lives in the slot, so a
+//     worker still busy with a stalled batch reads the pool's memory, not the caller's.
+//
+// The row decomposition changes no result: every output row is one tsx_cpu_gu_rows / tsx_cpu_down_rows row, whichever
+// thread computes it, and h is quantized from complete rows.
+#include <linux/futex.h>
 #include <sched.h>
+#include <sys/syscall.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <atomic>
 #include <chrono>
+#include <climits>
 #include <cmath>
-#include <condition_variable>
 #include <cstdio>
+#include <ctime>
 #include <memory>
-#include <mutex>
 #include <set>
 #include <thread>
 #include <utility>
@@ -48,13 +60,23 @@ void cpu_quant(const float* x, int64_t n, void* dst);
 namespace {
 
 using Clock = std::chrono::steady_clock;
-double ms_between(Clock::time_point a, Clock::time_point b) {
-    return std::chrono::duration<double, std::milli>(b - a).count();
+int64_t ns_since(Clock::time_point a) {
+    return std::chrono::duration_cast<std::chrono::nanoseconds>(Clock::now() - a).count();
 }
 inline void cpu_relax() {
 #if defined(__x86_64__) || defined(__i386__)
     __builtin_ia32_pause();
 #endif
+}
+
+// Sleep while *word == expected (at most `ms`), and wake every sleeper of *word.
+void futex_sleep(std::atomic<uint32_t>* word, uint32_t expected, int ms) {
+    static_assert(sizeof(std::atomic<uint32_t>) == sizeof(uint32_t), "a futex word is 32 bits");
+    timespec ts{ms / 1000, (long) (ms % 1000) * 1000000L};
+    syscall(SYS_futex, reinterpret_cast<uint32_t*>(word), FUTEX_WAIT_PRIVATE, expected, &ts, nullptr, 0);
+}
+void futex_wake_all(std::atomic<uint32_t>* word) {
+    syscall(SYS_futex, reinterpret_cast<uint32_t*>(word), FUTEX_WAKE_PRIVATE, INT_MAX, nullptr, nullptr, 0);
 }
 
 // One logical CPU per physical core the process may run on (Linux sysfs topology), in CPU order; empty when the
@@ -85,295 +107,256 @@ std::vector<int> physical_cores() {
     return out;
 }
 
-constexpr uint64_t pack_head(uint32_t epoch, uint32_t n, uint32_t i) {
-    return (uint64_t) epoch << 32 | (uint64_t) (n & 0xFFFFu) << 16 | (i & 0xFFFFu);
-}
+// An expert's claim state inside a batch: a cache line each, so threads on different experts never contend.
+struct alignas(64) ExpertCursor {
+    std::atomic<int32_t> gu_next{0};  // next gate/up chunk to hand out
+    std::atomic<int32_t> gu_done{0};  // gate/up chunks completed
+    std::atomic<int32_t> dn_next{0};  // next down chunk to hand out
+    std::atomic<int32_t> open{0};     // 1 once h is quantized: the down chunks may be taken
+};
+
+// One batch: its description (written by the host while no worker is attached) and its counters.
+struct Slot {
+    alignas(64) std::atomic<int32_t> attached{0};
+    alignas(64) std::atomic<int32_t> finished{0};   // chunks completed
+    alignas(64) std::atomic<int32_t> unclaimed{0};  // chunks not handed out yet
+    alignas(64) uint64_t seq = 0;
+    tsx_cpu_fmt f{};
+    int nb = 0, gu_chunks = 1, dn_chunks = 1, total = 0;
+    tsx_cpu_job jobs[TSX_POOL_MAX_SPLIT];
+    ExpertCursor cur[TSX_POOL_MAX_SPLIT];
+    std::vector<float> ff;    // [nb][TSX_CPU_MAXT][n_ff]: SwiGLU rows
+    std::vector<uint8_t> hq;  // [nb][TSX_CPU_MAXT][h_bytes]: their Q8_1
+
+    float* ff_row(int e, int t) { return ff.data() + ((size_t) e * TSX_CPU_MAXT + t) * (size_t) f.n_ff; }
+    uint8_t* hq_row(int e, int t) { return hq.data() + ((size_t) e * TSX_CPU_MAXT + t) * (size_t) f.h_bytes; }
+};
+
+// a worker's state for tsx_pool_diag; values >= 0 are the expert it works on
+constexpr int32_t kIdle = -1, kSleeping = -2, kWaitingH = -3;
 
 }  // namespace
 
 struct tsx_pool {
-    enum Mode { kNone = 0, kGateUp = 1, kDown = 2, kFused = 3 };
-
     int n_ = 0;
     bool host_works_ = true;
     int tasks_ = 0;
-    std::atomic<int64_t> spin_us_{20000};   // set between runs, read by parked workers
+    std::atomic<int64_t> spin_us_{20000};  // set between runs, read by idle workers
     std::atomic<int64_t> stall_ms_{60000};
 
-    alignas(64) std::atomic<uint64_t> head_{0};
-    alignas(64) std::atomic<uint32_t> done_{0};
-    alignas(64) std::atomic<uint32_t> parked_{0};
-    alignas(64) std::atomic<uint32_t> epoch_{0};
-    alignas(64) std::atomic<uint32_t> sleepers_{0};
+    alignas(64) std::atomic<uint64_t> current_{0};  // sequence number of the batch on offer (0: none yet)
+    alignas(64) std::atomic<uint32_t> bell_{0};     // futex word: bumped on every publish and at shutdown
+    alignas(64) std::atomic<int32_t> sleepers_{0};
     alignas(64) std::atomic<bool> stop_{false};
     std::atomic<bool> failed_{false};
-    std::mutex mu_;
-    std::condition_variable cv_;
+    uint64_t seq_ = 0;  // host only: the last batch published
+    Slot slot_[2];
     std::vector<std::thread> threads_;
-    // each worker's state for tsx_pool_diag: parked, sleeping, between batches, or the job it runs
-    static constexpr int32_t kParked = -1, kSleeping = -2, kBetween = -3;
-    struct alignas(64) WState {  // a line each: a worker's stores never contend with another's
-        std::atomic<int32_t> v{kParked};
+    struct alignas(64) WState {
+        std::atomic<int32_t> v{kIdle};
     };
     std::unique_ptr<WState[]> wstate_;
-
-    // the current batch: written by the host before it publishes, read by the workers after their acquire
-    Mode mode_ = kNone;
-    const tsx_cpu_fmt* f_ = nullptr;
-    const tsx_cpu_job* jobs_ = nullptr;
-    int64_t rows_ = 0;
-    int ntasks_ = 1, gu_parts_ = 1, down_parts_ = 1, nb_ = 0;
-    std::vector<float> ff_;      // [TSX_POOL_MAX_SPLIT][MAXT][n_ff]
-    std::vector<uint8_t> hq_;    // [TSX_POOL_MAX_SPLIT][MAXT][h_bytes]
-    struct alignas(64) Ready {
-        std::atomic<int> gu_left{0};
-        std::atomic<bool> ready{false};
-    };
-    std::unique_ptr<Ready[]> ready_{new Ready[TSX_POOL_MAX_SPLIT]};
     std::vector<uint8_t> acts_;  // the hybrid call's quantized token rows
 
-    // statistics (host thread only)
-    double ms_park_ = 0, ms_drain_ = 0, ms_gu_ = 0, ms_q_ = 0, ms_down_ = 0, ms_fused_ = 0;
+    // statistics: [0] waiting for a slot's workers to leave, [1] batches from publish to finished (host);
+    // [2] gate/up rows, [3] quantizing h, [4] down rows, [5] spinning with nothing open (all threads, summed)
+    std::atomic<int64_t> ns_[6] = {};
     int64_t bytes_ = 0;
 
-    float* ff_row(int e, int t) { return ff_.data() + ((size_t) e * TSX_CPU_MAXT + t) * (size_t) f_->n_ff; }
-    uint8_t* hq_row(int e, int t) { return hq_.data() + ((size_t) e * TSX_CPU_MAXT + t) * (size_t) f_->h_bytes; }
+    void add_ns(int i, int64_t v) { ns_[i].fetch_add(v, std::memory_order_relaxed); }
+    void set_state(int id, int32_t v) {
+        if (id >= 0) wstate_[id].v.store(v, std::memory_order_relaxed);
+    }
 
-    // ---- the protocol
-    void publish() {
-        epoch_.fetch_add(1, std::memory_order_seq_cst);
-        if (sleepers_.load(std::memory_order_seq_cst) != 0) {
-            std::lock_guard<std::mutex> lk(mu_);
-            cv_.notify_all();
-        }
-    }
-    uint32_t begin_batch(int n) {
-        done_.store(0, std::memory_order_relaxed);
-        const uint32_t e = epoch_.load(std::memory_order_relaxed) + 1;  // only the host bumps the epoch
-        head_.store(pack_head(e, (uint32_t) n, 0), std::memory_order_release);
-        publish();
-        return e;
-    }
-    int claim(uint32_t epoch) {
-        uint64_t h = head_.load(std::memory_order_acquire);
-        for (;;) {
-            if ((uint32_t) (h >> 32) != epoch) return -1;  // another batch than the one this thread woke for
-            const uint32_t n = (uint32_t) (h >> 16) & 0xFFFFu, i = (uint32_t) h & 0xFFFFu;
-            if (i >= n) return -1;
-            if (head_.compare_exchange_weak(h, h + 1, std::memory_order_acq_rel, std::memory_order_acquire))
-                return (int) i;
+    // ---- the workers
+    uint64_t next_batch(uint64_t seen, int id) {  // 0 when stopping
+        set_state(id, kIdle);
+        const auto t0 = Clock::now();
+        for (uint32_t spins = 1;; ++spins) {
+            if (stop_.load(std::memory_order_acquire)) return 0;
+            const uint64_t c = current_.load(std::memory_order_acquire);
+            if (c != seen) return c;
+            cpu_relax();
+            if (spins % 256) continue;
+            if (ns_since(t0) < spin_us_.load(std::memory_order_relaxed) * 1000) {
+                if (spins % 4096 == 0) std::this_thread::yield();
+                continue;
+            }
+            set_state(id, kSleeping);
+            sleepers_.fetch_add(1, std::memory_order_seq_cst);
+            const uint32_t b = bell_.load(std::memory_order_seq_cst);
+            if (current_.load(std::memory_order_seq_cst) == seen && !stop_.load(std::memory_order_seq_cst))
+                futex_sleep(&bell_, b, 100);
+            sleepers_.fetch_sub(1, std::memory_order_relaxed);
+            set_state(id, kIdle);
         }
     }
     void worker(int id) {
-        uint32_t seen = 0;
-        wstate_[id].v.store(kParked, std::memory_order_relaxed);
-        parked_.fetch_add(1, std::memory_order_acq_rel);  // parked from the start: the first run waits for that
+        uint64_t seen = 0;
         for (;;) {
-            const auto parked_at = Clock::now();
-            auto yield_at = parked_at + std::chrono::microseconds(50);
-            uint32_t spins = 0;
-            while (epoch_.load(std::memory_order_acquire) == seen) {
-                if (stop_.load(std::memory_order_relaxed)) return;
-                cpu_relax();
-                if ((++spins & 63u) != 0) continue;
-                const auto now = Clock::now();
-                if (now - parked_at < std::chrono::microseconds(spin_us_.load(std::memory_order_relaxed))) {
-                    if (now >= yield_at) {
-                        std::this_thread::yield();
-                        yield_at = now + std::chrono::microseconds(50);
+            const uint64_t s = next_batch(seen, id);
+            if (s == 0) return;
+            seen = s;
+            Slot& S = slot_[s & 1];
+            S.attached.fetch_add(1, std::memory_order_seq_cst);
+            if (current_.load(std::memory_order_seq_cst) == s) work(S, id);
+            S.attached.fetch_sub(1, std::memory_order_release);
+        }
+    }
+
+    // ---- the work of one batch, for a worker (id >= 0) or the host (id = -1)
+    void work(Slot& S, int id) {
+        const int nb = S.nb, G = S.gu_chunks, D = S.dn_chunks;
+        const int threads = n_ + (host_works_ ? 1 : 0);
+        int at = (int) ((int64_t) (id + 1) * nb / std::max(1, threads));  // threads start spread over the experts
+        Clock::time_point idle_since{};
+        bool idle = false;
+        while (S.unclaimed.load(std::memory_order_acquire) > 0) {
+            bool did = false;
+            for (int i = 0; i < nb && !did; ++i) {
+                const int e = (at + i) % nb;
+                ExpertCursor& X = S.cur[e];
+                if (X.gu_next.load(std::memory_order_relaxed) < G) {
+                    const int c = X.gu_next.fetch_add(1, std::memory_order_relaxed);
+                    if (c >= G) continue;
+                    did = true;
+                    at = e;
+                    if (idle) add_ns(5, ns_since(idle_since)), idle = false;
+                    set_state(id, e);
+                    S.unclaimed.fetch_sub(1, std::memory_order_relaxed);
+                    gate_up_chunk(S, e, c);
+                    if (X.gu_done.fetch_add(1, std::memory_order_acq_rel) + 1 == G) {  // every row of h is in
+                        const auto t = Clock::now();
+                        for (int tk = 0; tk < S.jobs[e].nt; ++tk) tsx::cpu_quant(S.ff_row(e, tk), S.f.n_ff, S.hq_row(e, tk));
+                        add_ns(3, ns_since(t));
+                        X.open.store(1, std::memory_order_release);
                     }
-                    continue;
+                    S.finished.fetch_add(1, std::memory_order_release);
+                } else if (X.open.load(std::memory_order_acquire) && X.dn_next.load(std::memory_order_relaxed) < D) {
+                    const int c = X.dn_next.fetch_add(1, std::memory_order_relaxed);
+                    if (c >= D) continue;
+                    did = true;
+                    at = e;
+                    if (idle) add_ns(5, ns_since(idle_since)), idle = false;
+                    set_state(id, e);
+                    S.unclaimed.fetch_sub(1, std::memory_order_relaxed);
+                    down_chunk(S, e, c);
+                    S.finished.fetch_add(1, std::memory_order_release);
                 }
-                std::unique_lock<std::mutex> lk(mu_);
-                wstate_[id].v.store(kSleeping, std::memory_order_relaxed);
-                sleepers_.fetch_add(1, std::memory_order_seq_cst);
-                cv_.wait(lk, [&] {
-                    return epoch_.load(std::memory_order_seq_cst) != seen || stop_.load(std::memory_order_relaxed);
-                });
-                sleepers_.fetch_sub(1, std::memory_order_relaxed);
-                wstate_[id].v.store(kParked, std::memory_order_relaxed);
             }
-            if (stop_.load(std::memory_order_acquire)) return;
-            seen = epoch_.load(std::memory_order_acquire);
-            parked_.fetch_sub(1, std::memory_order_acq_rel);
-            wstate_[id].v.store(kBetween, std::memory_order_relaxed);
-            drain(seen, id);
-            wstate_[id].v.store(kParked, std::memory_order_relaxed);
-            parked_.fetch_add(1, std::memory_order_acq_rel);
+            if (did) continue;
+            // every chunk left waits for an h that another thread is making
+            if (!idle) idle = true, idle_since = Clock::now(), set_state(id, kWaitingH);
+            if (failed_.load(std::memory_order_relaxed) || stop_.load(std::memory_order_relaxed)) break;
+            cpu_relax();
         }
+        if (idle) add_ns(5, ns_since(idle_since));
     }
-    void drain(uint32_t epoch, int id = -1) {
-        for (int i; (i = claim(epoch)) >= 0;) {
-            if (id >= 0) wstate_[id].v.store(i, std::memory_order_relaxed);
-            run_task(i);
-            done_.fetch_add(1, std::memory_order_release);
-        }
+    void gate_up_chunk(Slot& S, int e, int c) {
+        const auto t = Clock::now();
+        const tsx_cpu_job& j = S.jobs[e];
+        const int FF = (int) S.f.n_ff;
+        float* ff[TSX_CPU_MAXT];
+        for (int tk = 0; tk < j.nt; ++tk) ff[tk] = S.ff_row(e, tk);
+        tsx::cpu_gu_rows(S.f, j.blob, j.act, j.nt, ff, (int) ((int64_t) FF * c / S.gu_chunks),
+                         (int) ((int64_t) FF * (c + 1) / S.gu_chunks));
+        add_ns(2, ns_since(t));
     }
-    // a bounded wait: false (and the pool failed) after `stall_` without progress
+    void down_chunk(Slot& S, int e, int c) {
+        const auto t = Clock::now();
+        const tsx_cpu_job& j = S.jobs[e];
+        const int N = (int) S.f.n_embd;
+        const void* hq[TSX_CPU_MAXT];
+        for (int tk = 0; tk < j.nt; ++tk) hq[tk] = S.hq_row(e, tk);
+        tsx::cpu_down_rows(S.f, j.blob, hq, j.nt, j.out, (int) ((int64_t) N * c / S.dn_chunks),
+                           (int) ((int64_t) N * (c + 1) / S.dn_chunks));
+        add_ns(4, ns_since(t));
+    }
+
+    // ---- the host
+    // Waits for done(); false (and the pool failed) when progress() stays unchanged for the stall limit.
     template <typename Done, typename Progress>
     bool bounded_wait(Done done, Progress progress, const char* what) {
-        uint32_t spins = 0, last = progress();
+        int64_t last = progress();
         auto t0 = Clock::now();
-        while (!done()) {
+        for (uint32_t spins = 1; !done(); ++spins) {
             cpu_relax();
-            if ((++spins & 1023u) != 0) continue;
-            if (failed_.load(std::memory_order_relaxed)) return false;
-            const uint32_t p = progress();
-            const auto now = Clock::now();
+            if (spins % 1024) continue;
+            const int64_t p = progress();
             if (p != last) {
                 last = p;
-                t0 = now;
-            } else if (now - t0 > std::chrono::milliseconds(stall_ms_.load(std::memory_order_relaxed))) {
-                tsx::set_error("tsx_pool: stalled %s (%u of %d jobs done, %u of %d workers parked)", what,
-                               done_.load(), ntasks_, parked_.load(), n_);
+                t0 = Clock::now();
+            } else if (ns_since(t0) > stall_ms_.load(std::memory_order_relaxed) * 1000000) {
+                tsx::set_error("tsx_pool: no progress for %lld ms while %s", (long long) stall_ms_.load(), what);
                 failed_.store(true);
                 return false;
             }
         }
         return true;
     }
-    bool wait_parked(const char* what) {
-        return bounded_wait([&] { return parked_.load(std::memory_order_acquire) == (uint32_t) n_; },
-                            [&] { return parked_.load(std::memory_order_relaxed); }, what);
+    int chunks_per_expert(int nb, int64_t rows) const {
+        const int per_phase = tasks_ > 0 ? tasks_ : 3 * (n_ + (host_works_ ? 1 : 0));
+        return (int) std::clamp<int64_t>((per_phase + nb - 1) / nb, 1, rows);
     }
-    bool run_phase(Mode mode, int n) {
-        const auto a = Clock::now();
-        if (!wait_parked("before a phase")) return false;
-        const auto b = Clock::now();
-        mode_ = mode;
-        ntasks_ = n;
-        const uint32_t e = begin_batch(n);
-        if (host_works_) drain(e);
-        const bool ok = bounded_wait([&] { return done_.load(std::memory_order_acquire) >= (uint32_t) n; },
-                                     [&] { return done_.load(std::memory_order_relaxed); }, "draining a phase") &&
-                        wait_parked("after a phase");
-        const auto c = Clock::now();
-        ms_park_ += ms_between(a, b);
-        ms_drain_ += ms_between(b, c);
-        return ok;
-    }
-
-    // ---- the work
-    void rows_task(int i) {  // gate/up or down rows [g0, g1) of the batch's experts, one after another
-        const tsx_cpu_fmt& f = *f_;
-        const int per = mode_ == kGateUp ? (int) f.n_ff : (int) f.n_embd;
-        const int64_t g0 = rows_ * i / ntasks_, g1 = rows_ * (i + 1) / ntasks_;
-        for (int64_t r = g0; r < g1;) {
-            const int e = (int) (r / per), r0 = (int) (r % per);
-            const int r1 = (int) std::min<int64_t>(per, r0 + (g1 - r));
-            expert_rows(e, mode_ == kGateUp, r0, r1);
-            r += r1 - r0;
+    int run_batch(const tsx_cpu_fmt& f, const tsx_cpu_job* jobs, int nb) {
+        const uint64_t s = seq_ + 1;
+        Slot& S = slot_[s & 1];
+        const auto t0 = Clock::now();
+        // workers that joined this slot's previous batch (two batches back) must have left before it is rewritten
+        if (!bounded_wait([&] { return S.attached.load(std::memory_order_seq_cst) == 0; },
+                          [&] { return (int64_t) S.attached.load(std::memory_order_relaxed); },
+                          "waiting for workers to leave a finished batch"))
+            return TSX_ERR_STALLED;
+        const auto t1 = Clock::now();
+        S.f = f;
+        S.nb = nb;
+        std::copy(jobs, jobs + nb, S.jobs);
+        S.gu_chunks = chunks_per_expert(nb, f.n_ff);
+        S.dn_chunks = chunks_per_expert(nb, f.n_embd);
+        S.total = nb * (S.gu_chunks + S.dn_chunks);
+        const size_t ffn = (size_t) nb * TSX_CPU_MAXT * (size_t) f.n_ff;
+        const size_t hqn = (size_t) nb * TSX_CPU_MAXT * (size_t) f.h_bytes;
+        if (S.ff.size() < ffn) S.ff.resize(ffn);
+        if (S.hq.size() < hqn) S.hq.resize(hqn);
+        for (int e = 0; e < nb; ++e) {
+            S.cur[e].gu_next.store(0, std::memory_order_relaxed);
+            S.cur[e].gu_done.store(0, std::memory_order_relaxed);
+            S.cur[e].dn_next.store(0, std::memory_order_relaxed);
+            S.cur[e].open.store(0, std::memory_order_relaxed);
         }
-    }
-    void expert_rows(int e, bool gate_up, int r0, int r1) {
-        const tsx_cpu_job& j = jobs_[e];
-        if (gate_up) {
-            float* ff[TSX_CPU_MAXT];
-            for (int t = 0; t < j.nt; ++t) ff[t] = ff_row(e, t);
-            tsx::cpu_gu_rows(*f_, j.blob, j.act, j.nt, ff, r0, r1);
-        } else {
-            const void* hq[TSX_CPU_MAXT];
-            for (int t = 0; t < j.nt; ++t) hq[t] = hq_row(e, t);
-            tsx::cpu_down_rows(*f_, j.blob, hq, j.nt, j.out, r0, r1);
-        }
-    }
-    void quant_h(int e) {
-        for (int t = 0; t < jobs_[e].nt; ++t) tsx::cpu_quant(ff_row(e, t), f_->n_ff, hq_row(e, t));
-    }
-    void run_task(int i) {
-        if (mode_ != kFused) {
-            rows_task(i);
-            return;
-        }
-        // gate/up tasks first (index order), then down tasks: a down task waits only for gate/up tasks that are
-        // already running
-        const int gu_tasks = nb_ * gu_parts_;
-        if (i < gu_tasks) {
-            const int e = i / gu_parts_, part = i % gu_parts_;
-            const int FF = (int) f_->n_ff;
-            expert_rows(e, true, FF * part / gu_parts_, FF * (part + 1) / gu_parts_);
-            if (ready_[e].gu_left.fetch_sub(1, std::memory_order_acq_rel) == 1) {  // the expert's last rows: h
-                quant_h(e);
-                ready_[e].ready.store(true, std::memory_order_release);
-            }
-            return;
-        }
-        const int d = i - gu_tasks, e = d / down_parts_, part = d % down_parts_;
-        if (!ready_[e].ready.load(std::memory_order_acquire) &&
-            !bounded_wait([&] { return ready_[e].ready.load(std::memory_order_acquire); },
-                          [&] { return done_.load(std::memory_order_relaxed); }, "waiting for an expert's h"))
-            return;
-        const int N = (int) f_->n_embd;
-        expert_rows(e, false, N * part / down_parts_, N * (part + 1) / down_parts_);
-    }
-    int phase_tasks(int64_t rows) const {
-        const int t = tasks_ == 0 ? 3 * (n_ + (host_works_ ? 1 : 0)) : tasks_;
-        return (int) std::max<int64_t>(1, std::min<int64_t>(rows, t));
-    }
-
-    int stalled() {
-        if (*tsx::error_cstr() == 0) tsx::set_error("tsx_pool: a worker stalled waiting for an expert's h");
-        return TSX_ERR_STALLED;
+        S.finished.store(0, std::memory_order_relaxed);
+        S.unclaimed.store(S.total, std::memory_order_relaxed);
+        S.seq = s;
+        seq_ = s;
+        // publish: the description above happens-before any worker's read of it (its seq_cst load of current_)
+        current_.store(s, std::memory_order_seq_cst);
+        bell_.fetch_add(1, std::memory_order_seq_cst);
+        if (sleepers_.load(std::memory_order_seq_cst) > 0) futex_wake_all(&bell_);
+        if (host_works_) work(S, -1);
+        const bool ok =
+            bounded_wait([&] { return S.finished.load(std::memory_order_acquire) == S.total; },
+                         [&] { return (int64_t) S.finished.load(std::memory_order_relaxed); }, "running a batch");
+        add_ns(0, std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count());
+        add_ns(1, ns_since(t1));
+        return ok ? (int) TSX_OK : (int) TSX_ERR_STALLED;
     }
     int run(const tsx_cpu_fmt& f, const tsx_cpu_job* jobs, int n) {
         if (failed_.load()) {
             tsx::set_error("tsx_pool: the pool stalled earlier and takes no more work");
             return TSX_ERR_STALLED;
         }
-        f_ = &f;
-        const size_t ffn = (size_t) TSX_POOL_MAX_SPLIT * TSX_CPU_MAXT * (size_t) f.n_ff;
-        const size_t hqn = (size_t) TSX_POOL_MAX_SPLIT * TSX_CPU_MAXT * (size_t) f.h_bytes;
-        if (ff_.size() < ffn) ff_.resize(ffn);
-        if (hq_.size() < hqn) hq_.resize(hqn);
-        const int participants = n_ + (host_works_ ? 1 : 0);
         for (int b0 = 0; b0 < n; b0 += TSX_POOL_MAX_SPLIT) {
-            const int nb = std::min(TSX_POOL_MAX_SPLIT, n - b0);
-            jobs_ = jobs + b0;
-            nb_ = nb;
-            if (nb > 1 && participants > 1) {  // dependent gate/up and down tasks per expert
-                const auto a = Clock::now();
-                // the reference's split of the tasks between the phases by their weight bytes (pool.cpp:782-788)
-                const double gu_share =
-                    (double) (2 * f.up_off) / (double) (2 * f.up_off + f.d_row * (uint64_t) f.n_embd);
-                const int target = 2 * phase_tasks((int64_t) nb * (f.n_ff + f.n_embd));
-                gu_parts_ = (int) std::min<int64_t>(f.n_ff, std::max(1L, std::lround(target * gu_share / nb)));
-                down_parts_ =
-                    (int) std::min<int64_t>(f.n_embd, std::max(1L, std::lround(target * (1.0 - gu_share) / nb)));
-                while ((int64_t) nb * (gu_parts_ + down_parts_) > 0xFFFF) {
-                    gu_parts_ = std::max(1, gu_parts_ / 2);
-                    down_parts_ = std::max(1, down_parts_ / 2);
-                }
-                for (int e = 0; e < nb; ++e) {
-                    ready_[e].gu_left.store(gu_parts_, std::memory_order_relaxed);
-                    ready_[e].ready.store(false, std::memory_order_relaxed);
-                }
-                if (!run_phase(kFused, nb * (gu_parts_ + down_parts_)) || failed_.load()) return stalled();
-                ms_fused_ += ms_between(a, Clock::now());
-                continue;
-            }
-            const auto a = Clock::now();
-            rows_ = (int64_t) nb * f.n_ff;
-            if (!run_phase(kGateUp, phase_tasks(rows_))) return stalled();
-            const auto b = Clock::now();
-            for (int e = 0; e < nb; ++e) quant_h(e);
-            const auto c = Clock::now();
-            rows_ = (int64_t) nb * f.n_embd;
-            if (!run_phase(kDown, phase_tasks(rows_))) return stalled();
-            ms_gu_ += ms_between(a, b);
-            ms_q_ += ms_between(b, c);
-            ms_down_ += ms_between(c, Clock::now());
+            const int rc = run_batch(f, jobs + b0, std::min(TSX_POOL_MAX_SPLIT, n - b0));
+            if (rc != TSX_OK) return rc;
         }
-        mode_ = kNone;
         bytes_ += (int64_t) n * (int64_t) f.bytes;
         return TSX_OK;
     }
 
     void shutdown() {
         stop_.store(true, std::memory_order_seq_cst);
-        {
-            std::lock_guard<std::mutex> lk(mu_);
-            cv_.notify_all();
-        }
+        bell_.fetch_add(1, std::memory_order_seq_cst);
+        futex_wake_all(&bell_);
         for (auto& t : threads_) t.join();
         threads_.clear();
     }
@@ -441,8 +424,7 @@ TSX_API int tsx_pool_run(tsx_pool* p, const tsx_cpu_fmt* f, const tsx_cpu_job* j
 TSX_API int tsx_pool_stats(const tsx_pool* p, double* ms6, int64_t* bytes) {
     clear_error();
     TSX_REQUIRE(p && ms6, "tsx_pool_stats: pool and ms6");
-    const double v[6] = {p->ms_park_, p->ms_drain_, p->ms_gu_, p->ms_q_, p->ms_down_, p->ms_fused_};
-    for (int i = 0; i < 6; ++i) ms6[i] = v[i];
+    for (int i = 0; i < 6; ++i) ms6[i] = (double) p->ns_[i].load() * 1e-6;
     if (bytes) *bytes = p->bytes_;
     return TSX_OK;
 }
@@ -450,17 +432,21 @@ TSX_API int tsx_pool_stats(const tsx_pool* p, double* ms6, int64_t* bytes) {
 TSX_API int tsx_pool_diag(const tsx_pool* p, char* buf, size_t n) {
     clear_error();
     TSX_REQUIRE(p && buf && n > 0, "tsx_pool_diag: pool and a buffer");
-    const uint64_t h = p->head_.load();
-    int w = std::snprintf(buf, n, "epoch %u head epoch %u jobs %u next %u done %u parked %u/%d sleepers %u%s; workers:",
-                          p->epoch_.load(), (uint32_t) (h >> 32), (uint32_t) (h >> 16) & 0xFFFFu,
-                          (uint32_t) h & 0xFFFFu, p->done_.load(), p->parked_.load(), p->n_, p->sleepers_.load(),
-                          p->failed_.load() ? " FAILED" : "");
+    const uint64_t c = p->current_.load();
+    const Slot& S = p->slot_[c & 1];
+    int idle = 0;
+    for (int i = 0; i < p->n_; ++i) idle += p->wstate_[i].v.load() == kIdle || p->wstate_[i].v.load() == kSleeping;
+    int w = std::snprintf(buf, n,
+                          "batch %llu: %d experts, %d/%d chunks finished, %d unclaimed, attached %d|%d; idle %d/%d, "
+                          "sleepers %d%s; workers:",
+                          (unsigned long long) c, c ? S.nb : 0, c ? S.finished.load() : 0, c ? S.total : 0,
+                          c ? S.unclaimed.load() : 0, p->slot_[0].attached.load(), p->slot_[1].attached.load(), idle,
+                          p->n_, p->sleepers_.load(), p->failed_.load() ? " FAILED" : "");
     for (int i = 0; i < p->n_ && w > 0 && (size_t) w < n; ++i) {
         const int32_t st = p->wstate_[i].v.load();
-        const char* name = st == tsx_pool::kParked ? "parked" : st == tsx_pool::kSleeping ? "sleeping"
-                           : st == tsx_pool::kBetween ? "between" : nullptr;
+        const char* name = st == kIdle ? "idle" : st == kSleeping ? "sleeping" : st == kWaitingH ? "waiting-h" : nullptr;
         w += name ? std::snprintf(buf + w, n - (size_t) w, " %s", name)
-                  : std::snprintf(buf + w, n - (size_t) w, " job %d", st);
+                  : std::snprintf(buf + w, n - (size_t) w, " expert %d", st);
     }
     return TSX_OK;
 }
@@ -486,6 +472,10 @@ TSX_API int tsx_moe_hybrid_cpu(tsx_pool* p, const tsx_cpu_fmt* f, const uint8_t*
     TSX_REQUIRE(p && f && f->gu_act == 9 && host_blobs && stride >= f->bytes && slot_of && n_expert > 0 && k >= 1 &&
                     n_tok >= 0 && ids && x && cpu_out && miss && n_miss,
                 "tsx_moe_hybrid_cpu: pool, format, host blobs (stride >= blob bytes), slot_of, ids, x, outputs");
+    if (p->failed_.load()) {  // workers may still read the stalled batch's token rows in acts_
+        set_error("tsx_pool: the pool stalled earlier and takes no more work");
+        return TSX_ERR_STALLED;
+    }
     const int n_ent = n_tok * k;
     const int64_t N = f->n_embd;
     std::vector<char> quantized((size_t) n_tok, 0);
@@ -534,6 +524,9 @@ TSX_API int tsx_moe_hybrid_decode_layer(tsx_pool* p, const tsx_cpu_fmt* f, tsx_h
                     (!a->shared || (a->sgate && a->sh_gate && a->sh_up && a->sh_hq && a->sh_out)),
                 "tsx_moe_hybrid_decode_layer: a null buffer, or n_tok outside 1..8");
     const tsx_expert_layout& L = a->L;
+    TSX_REQUIRE(f->n_embd == L.n_embd && f->n_ff == L.n_ff && f->gu_type == L.gu_type && f->d_type == L.d_type &&
+                    f->up_off == L.up_off && f->down_off == L.down_off && a->stride >= f->bytes,
+                "tsx_moe_hybrid_decode_layer: the CPU format does not describe the layer's experts");
     const int T = a->n_tok, k = a->k, n_ent = T * k, N = (int) L.n_embd, FF = (int) L.n_ff;
     const hipStream_t st = (hipStream_t) stream;
     // one event per calling thread and device (an event records only on a stream of its own device)

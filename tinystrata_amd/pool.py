@@ -1,5 +1,5 @@
 """The hybrid CPU/GPU expert split through libtsx_moe's C ABI (include/tsx_pool.h): the CPU expert rows, the worker
-pool with the reference's epoch-CAS claim protocol, and a decode MoE layer whose experts without an HBM slot run on
+pool (two batch slots joined by attach-and-recheck, per-expert chunk cursors), and a decode MoE layer whose experts without an HBM slot run on
 the pool while the GPU runs the resident ones.
 
 Mirrors strata::kernels::cpu::ExpertPool (include/strata/kernels/cpu/pool.hpp:111-260), the native expert rows
@@ -15,7 +15,7 @@ import numpy as np
 import torch
 
 from . import ops
-from ._lib import CPU_MAXT, CpuFmt, CpuJob, HybridLayerArgs, check, lib
+from ._lib import CPU_MAXT, TSX_ERR_STALLED, CpuFmt, CpuJob, HybridLayerArgs, check, lib
 from .moe import MoEWeights
 
 
@@ -74,6 +74,7 @@ class ExpertPool:
         h = C.c_void_p()
         check(lib().tsx_pool_create(n_workers, int(pin), int(host_works), tasks, C.byref(h)), "pool create")
         self._h = h
+        self._stalled = []
 
     @property
     def handle(self) -> C.c_void_p:
@@ -111,21 +112,25 @@ class ExpertPool:
                 assert outs[t].dtype == np.float32 and outs[t].flags.c_contiguous
                 arr[i].act[t] = _ptr(acts[t])
                 arr[i].out[t] = _ptr(outs[t])
-        self._last = (arr, jobs)  # workers of a stalled run may still read them: kept until the next run or close()
-        check(lib().tsx_pool_run(self._h, C.byref(f), arr, len(jobs)), "pool run")
+        rc = lib().tsx_pool_run(self._h, C.byref(f), arr, len(jobs))
+        if rc == TSX_ERR_STALLED:
+            # the library copied the job table, but workers of the stalled batch may still read these tokens' rows
+            # and write their outputs: every array of such a run stays alive until close() has joined the workers
+            self._stalled.append(jobs)
+        check(rc, "pool run")
 
     def stats(self) -> dict:
         ms = (C.c_double * 6)()
         b = C.c_int64()
         check(lib().tsx_pool_stats(self._h, ms, C.byref(b)), "pool stats")
-        keys = ("wait_park", "drain", "gate_up", "quant_h", "down", "fused")
+        keys = ("wait_slot", "drain", "gate_up", "quant_h", "down", "wait_h")
         return {**{k: ms[i] for i, k in enumerate(keys)}, "bytes": b.value}
 
     def close(self) -> None:
         if self._h:
             lib().tsx_pool_destroy(self._h)  # joins the workers
             self._h = C.c_void_p()
-        self._last = None
+        self._stalled = []
 
     def __enter__(self) -> "ExpertPool":
         return self
