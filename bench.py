@@ -65,7 +65,7 @@ def make_logits(rng, cfg, layers):
     return rng.normal(0, 1, (layers, T, E)).astype(np.float32)
 
 
-def main() -> int:
+def parse_args(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -73,24 +73,68 @@ def main() -> int:
     ap.add_argument("--config", default="decode", choices=sorted(CONFIGS))
     ap.add_argument("--eager", action="store_true", help="launch each step eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the prompt-chunk configurations measured after the default decode line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="before the timed region, run one plain fp32 copy kernel (out = in * 1) over this many MiB: "
                          "the known-size launch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
-    args = ap.parse_args()
+    return ap.parse_args(argv)
+
+
+def main() -> int:
+    args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU; --gpus N > 1 is not supported (the sharding plan is design only)",
               file=sys.stderr)
         return 2
+    cfg = CONFIGS[args.config]
+    if "resident" in cfg:
+        return run_hybrid(args, cfg)
+    res = run_config(args, args.config, cfg, args.steps, args.warmup, cpu=not args.no_cpu)
+    line = {
+        "metric": METRIC,
+        "value": res["value"],
+        "unit": "MoE-layer tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": res["config"],
+        "roofline": res["roofline"],
+        "cpu_baseline": res["cpu_baseline"],
+    }
+    if args.config == "decode" and not args.no_secondary:
+        # the metric's prefill half: the prompt configurations, each measured the same way (fewer layers and steps;
+        # not part of `value`)
+        sec = {}
+        for name in ("prefill_long", "prefill"):
+            r = run_config(args, name, CONFIGS[name], steps=8, warmup=2, cpu=False, layers=2)
+            sec[name] = {"workload": r["config"]["workload"], "value": r["value"], "unit": "MoE-layer tokens/s",
+                         "ms_per_step": r["ms_per_step"], "layer_us": r["config"]["layer_us"],
+                         "layer_hbm_frac": r["config"]["layer_hbm_frac"],
+                         "layer_int8_mfma_frac": r["config"]["layer_int8_mfma_frac"],
+                         "distinct_experts_per_layer": r["config"]["distinct_experts_per_layer"],
+                         "roofline": r["roofline"]}
+        line["secondary"] = sec
+    print(json.dumps(line), flush=True)
+    return 0
 
+
+def run_config(args, name, cfg, steps, warmup, cpu, layers=None):
+    """One configuration: synthetic weights and inputs in HBM, `steps` timed steps (graph replays unless --eager), the
+    dominant launch timed alone, and (cpu) the reference CPU path on this host."""
     import torch
 
     from tinystrata_amd import _lib, moe, ops
 
-    cfg = CONFIGS[args.config]
-    if "resident" in cfg:
-        return run_hybrid(args, cfg)
-    gu, d, N, FF, E, k, shared, T, layers = (cfg[key] for key in ("gu", "d", "N", "FF", "E", "k", "shared", "T", "layers"))
+    gu, d, N, FF, E, k, shared, T = (cfg[key] for key in ("gu", "d", "N", "FF", "E", "k", "shared", "T"))
+    layers = layers or cfg["layers"]
     prefill = T > 8
     dev = torch.device("cuda:0")
     _lib.check(_lib.lib().tsx_moe_init(0), "tsx_moe_init")
@@ -102,7 +146,7 @@ def main() -> int:
     distinct = 24
     pool = moe.synthetic_pool(L, distinct, seed=1234)
     pool_dev = torch.from_numpy(pool).to(dev)
-    log(f"bench: {distinct} distinct experts quantized in {time.time() - t0:.1f}s; "
+    log(f"bench {name}: {distinct} distinct experts quantized in {time.time() - t0:.1f}s; "
         f"{layers} layers x {E + int(shared)} blobs x {stride / 1e6:.3f} MB in HBM")
     rng = np.random.default_rng(7)
     Ws, orders, shared_idx = [], [], []
@@ -131,7 +175,7 @@ def main() -> int:
         for l in range(layers):
             mls[l](x, logits_d[l], sg_d[l] if shared else None, x)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     graph = None
@@ -144,7 +188,7 @@ def main() -> int:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             step()
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             graph.replay()
     torch.cuda.synchronize()
 
@@ -162,12 +206,13 @@ def main() -> int:
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         graph.replay() if graph is not None else step()
     end.record()
     torch.cuda.synchronize()
-    ms_step = start.elapsed_time(end) / args.steps
+    ms_step = start.elapsed_time(end) / steps
     value = layers * T / (ms_step / 1e3)
+    log(f"bench {name}: {ms_step:.4f} ms per step of {layers} layers")
 
     # algorithmic work: each distinct expert's blob once per layer, the fp32 input and output rows; int8 ops
     ids_host = [ml.ids.cpu().numpy() for ml in mls]
@@ -178,7 +223,7 @@ def main() -> int:
     layer_s = ms_step / layers / 1e3
 
     # ---------------------------------------------------------------- the dominant launch, timed alone
-    reps = max(3, min(20, args.steps // 5))
+    reps = max(3, min(20, steps // 5))
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     if prefill and mls[0].fused_prefill:
@@ -239,53 +284,40 @@ def main() -> int:
     dom_s = ev0.elapsed_time(ev1) / (reps * layers) / 1e3
     achieved_gbs = dom_bytes / dom_s / 1e9
     achieved_tops = dom_ops / dom_s / 1e12
-    if prefill and args.config == "prefill_long":
+    if prefill and name == "prefill_long":
         roof = {"bound": "mfma", "achieved": round(achieved_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s (int8)",
                 "frac": round(achieved_tops / INT8_PEAK_TOPS, 4)}
     else:
         roof = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved_gbs / HBM_PEAK_GBS, 4)}
-    roof.update({"traffic": measured_traffic(args.config), "kernel": kernel, "launch_us": round(dom_s * 1e6, 3),
+    traffic = measured_traffic(name)
+    roof.update({"traffic": traffic, "kernel": kernel, "launch_us": round(dom_s * 1e6, 3),
                  "bytes_per_launch": int(dom_bytes), "int8_ops_per_launch": int(dom_ops),
+                 "traffic_over_algorithmic": round(traffic / dom_bytes, 3) if traffic else None,
                  "hbm_frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                  "int8_mfma_frac": round(achieved_tops / INT8_PEAK_TOPS, 4)})
 
-    # ---------------------------------------------------------------- the reference CPU path on this host
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared)
-
-    line = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "MoE-layer tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic",
-        "config": {
-            "workload": f"{args.config}: {cfg['desc']}",
-            "tokens": T, "layers": layers, "hidden": N, "expert_ff": FF, "experts": E, "top_k": k,
-            "shared_expert": shared, "graph": graph is not None,
-            "layer_us": round(layer_s * 1e6, 3),
-            "layer_hbm_GBps": round(float(np.mean(layer_bytes)) / layer_s / 1e9, 1),
-            "layer_hbm_frac": round(float(np.mean(layer_bytes)) / layer_s / 1e9 / HBM_PEAK_GBS, 4),
-            "layer_int8_TOPs": round(layer_ops / layer_s / 1e12, 3),
-            "layer_int8_mfma_frac": round(layer_ops / layer_s / 1e12 / INT8_PEAK_TOPS, 5),
-            "layer_bytes": int(np.mean(layer_bytes)),
-            "distinct_experts_per_layer": float(np.mean(distinct_per_layer)),
-            "layer_int8_ops": layer_ops,
-        },
-        "roofline": roof,
-        "cpu_baseline": cpu,
+    cpu_res = None
+    if cpu:
+        cpu_res = cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared)
+    config = {
+        "workload": f"{name}: {cfg['desc']}",
+        "tokens": T, "layers": layers, "hidden": N, "expert_ff": FF, "experts": E, "top_k": k,
+        "shared_expert": shared, "graph": graph is not None,
+        "layer_us": round(layer_s * 1e6, 3),
+        "layer_hbm_GBps": round(float(np.mean(layer_bytes)) / layer_s / 1e9, 1),
+        "layer_hbm_frac": round(float(np.mean(layer_bytes)) / layer_s / 1e9 / HBM_PEAK_GBS, 4),
+        "layer_int8_TOPs": round(layer_ops / layer_s / 1e12, 3),
+        "layer_int8_mfma_frac": round(layer_ops / layer_s / 1e12 / INT8_PEAK_TOPS, 5),
+        "layer_bytes": int(np.mean(layer_bytes)),
+        "distinct_experts_per_layer": float(np.mean(distinct_per_layer)),
+        "layer_int8_ops": layer_ops,
     }
-    print(json.dumps(line), flush=True)
-    return 0
+    del mls, Ws, graph, dom_graph
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"value": round(value, 2), "ms_per_step": round(ms_step, 4), "config": config, "roofline": roof,
+            "cpu_baseline": cpu_res}
 
 
 def run_hybrid(args, cfg) -> int:
@@ -365,57 +397,118 @@ def measured_traffic(config: str):
     return None if rec is None else rec.get("hbm_bytes_per_launch")
 
 
+# the CPU share of one GPU on the GPU boxes this bench runs on (their harness limits a job to 16 host threads per GPU)
+CPU_SHARE = 16
+
+
+def cpu_topology():
+    """This host's CPUs: model name, logical and physical counts (whole machine and this process's affinity mask), and
+    one logical CPU per physical core of the mask (sysfs topology), in CPU order."""
+    model = "unknown"
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    logical_all = os.cpu_count() or 1
+    mask = sorted(os.sched_getaffinity(0))
+    seen, cores = set(), []
+    phys_all = set()
+    for c in range(logical_all):
+        try:
+            core = int(open(f"/sys/devices/system/cpu/cpu{c}/topology/core_id").read())
+            pkg = int(open(f"/sys/devices/system/cpu/cpu{c}/topology/physical_package_id").read())
+        except (OSError, ValueError):
+            continue
+        phys_all.add((pkg, core))
+        if c in mask and (pkg, core) not in seen:
+            seen.add((pkg, core))
+            cores.append(c)
+    if not cores:
+        cores = mask
+    return {"model": model, "logical": logical_all, "physical": len(phys_all) or None,
+            "mask_logical": len(mask), "mask_physical": len(cores), "cores": cores}
+
+
 def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared):
-    """The reference CPU path (its own AVX-512/AVX2 expert rows, oracle/_ref) on this host's cores, over the same
-    routing and weights (each layer's used experts at distinct host addresses), timed for about cpu_seconds.  The
-    reference's pool takes at most 8 tokens per expert call, so a prompt chunk is sampled as its first 8 tokens."""
+    """The reference CPU path (its own AVX-512/AVX2 expert rows, oracle/_ref: Q8_K activations) on this host, one
+    pinned worker per physical core of the process's CPU mask (at most the GPU's host share), over the same routing
+    and weights (each layer's used experts at distinct host addresses), timed for about cpu_seconds.  The reference's
+    pool takes at most 8 tokens per expert call, so a prompt chunk is run as consecutive 8-token pieces (the first
+    64 tokens)."""
     import oracle as O
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    topo = cpu_topology()
+    threads = max(1, min(CPU_SHARE, topo["mask_physical"]))
+    cpus = np.asarray(topo["cores"][:threads], np.int32)
     stride = pool.shape[1]
     Tc = min(T, 8)
-    ids_host = [i[:Tc] for i in ids_host]
-    # per layer: only the experts it uses, remapped to 0..u-1, plus its shared blob
-    per = []
-    for l in range(layers):
-        used = np.unique(ids_host[l])
-        remap = {int(e): i for i, e in enumerate(used)}
-        blobs = [pool[orders[l][e]] for e in used]
-        if shared:
-            blobs.append(pool[shared_idx[l]])
-        per.append((np.stack(blobs), np.vectorize(remap.get)(ids_host[l]).astype(np.int32)))
-    umax = max(b.shape[0] for b, _ in per)
-    layer_stride = umax * stride
-    host = np.zeros((layers, umax, stride), np.uint8)
-    ids = np.zeros((layers, Tc, k), np.int32)
-    for l, (b, i) in enumerate(per):
-        host[l, : b.shape[0]] = b
-        ids[l] = i
-    wts = np.stack([ml.wts.cpu().numpy()[:Tc] for ml in mls]).astype(np.float32)
-    sgs = (1 / (1 + np.exp(-sg[:, :Tc].astype(np.float64)))).astype(np.float32)
+    pieces = [(t0, min(T, t0 + Tc)) for t0 in range(0, min(T, 64), Tc)]
     if not O.ref_available():
-        return cpu_port(L, per, Tc, k, shared, args.cpu_seconds)
-    shared_ptr = None
-    if shared:  # ref_moe_decode reads layer l's shared blob at shared + l * layer_stride: the last slot of every layer
+        per = []
         for l in range(layers):
-            host[l, umax - 1] = per[l][0][-1]
-        shared_ptr = host.ctypes.data + (umax - 1) * stride
-    x = np.ascontiguousarray(x0[:Tc])
+            used = np.unique(ids_host[l][:Tc])
+            blobs = [pool[orders[l][e]] for e in used] + ([pool[shared_idx[l]]] if shared else [])
+            per.append((np.stack(blobs), None))
+        return cpu_port(L, per, Tc, k, shared, args.cpu_seconds)
     R = O.ref()
-    one = R.ref_moe_decode(L.gu_type, L.d_type, L.n_embd, L.n_ff, Tc, k, layers, ids.ctypes.data, wts.ctypes.data,
-                           host.ctypes.data, stride, layer_stride, shared_ptr, sgs.ctypes.data, x.ctypes.data,
-                           threads, 2)
-    iters = int(max(3, min(5000, args.cpu_seconds / max(one * layers, 1e-6))))
-    x = np.ascontiguousarray(x0[:Tc])
-    per_layer = R.ref_moe_decode(L.gu_type, L.d_type, L.n_embd, L.n_ff, Tc, k, layers, ids.ctypes.data,
-                                 wts.ctypes.data, host.ctypes.data, stride, layer_stride, shared_ptr, sgs.ctypes.data,
-                                 x.ctypes.data, threads, iters)
+    wts_all = [ml.wts.cpu().numpy() for ml in mls]
+    runs = []
+    for a, b in pieces:
+        nt = b - a
+        per = []
+        for l in range(layers):  # only the experts this piece uses, remapped to 0..u-1, plus the layer's shared blob
+            ids_l = ids_host[l][a:b]
+            used = np.unique(ids_l)
+            remap = {int(e): i for i, e in enumerate(used)}
+            blobs = [pool[orders[l][e]] for e in used] + ([pool[shared_idx[l]]] if shared else [])
+            per.append((np.stack(blobs), np.vectorize(remap.get)(ids_l).astype(np.int32), len(used)))
+        umax = max(p[0].shape[0] for p in per)
+        host = np.zeros((layers, umax, stride), np.uint8)
+        ids = np.zeros((layers, nt, k), np.int32)
+        for l, (bl, i, _) in enumerate(per):
+            host[l, : bl.shape[0]] = bl
+            if shared:  # ref_moe_decode reads layer l's shared blob at shared + l * layer_stride: every layer's last slot
+                host[l, umax - 1] = bl[-1]
+            ids[l] = i
+        wts = np.ascontiguousarray(np.stack([w[a:b] for w in wts_all]).astype(np.float32))
+        sgs = np.ascontiguousarray((1 / (1 + np.exp(-sg[:, a:b].astype(np.float64)))).astype(np.float32))
+        shared_ptr = host.ctypes.data + (umax - 1) * stride if shared else None
+        x = np.ascontiguousarray(x0[a:b])
+        # algorithmic bytes of one pass: every layer's distinct experts (and the shared one) once, x in and out
+        nbytes = sum((u + int(shared)) * L.bytes + 2 * nt * L.n_embd * 4 for _, _, u in per)
+        runs.append((nt, host, ids, wts, sgs, shared_ptr, x, nbytes))
+
+    def one_pass(iters):
+        tot = 0.0
+        for nt, host, ids, wts, sgs, shared_ptr, x, _ in runs:
+            tot += R.ref_moe_decode(L.gu_type, L.d_type, L.n_embd, L.n_ff, nt, k, layers, ids.ctypes.data,
+                                    wts.ctypes.data, host.ctypes.data, stride, host.shape[1] * stride, shared_ptr,
+                                    sgs.ctypes.data, x.ctypes.data, threads, iters, cpus.ctypes.data) * layers
+        return tot  # seconds per pass over every piece, each the median of its iterations
+
+    first = one_pass(2)
+    iters = int(max(3, min(5000, args.cpu_seconds / max(first, 1e-6))))
+    sec = one_pass(iters)
+    toks = sum(r[0] for r in runs) * layers
+    nbytes = sum(r[7] for r in runs)
     isa = R.ref_isa()
-    return {"value": round(Tc / per_layer, 2), "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"{iters} passes x {layers} layers, median pass; reference iq{isa}/kq256 rows, "
-                      f"Q8_K activations, {threads} pinned threads, {Tc} token(s)"
-                      + (f" (the first {Tc} of the {T}-token chunk)" if Tc < T else ""),
-            "layer_us": round(per_layer * 1e6, 2)}
+    return {"value": round(toks / sec, 2), "unit": "MoE-layer tokens/s", "cores": threads, "kind": "reference",
+            "GBps": round(nbytes / sec / 1e9, 2),
+            "layer_us": round(sec / (len(runs) * layers) * 1e6, 2),
+            "cpu_model": topo["model"],
+            "host_cpus": {"logical": topo["logical"], "physical": topo["physical"],
+                          "mask_logical": topo["mask_logical"], "mask_physical": topo["mask_physical"]},
+            "isa": {512: "AVX-512 VNNI (iq512 rows)", 256: "AVX2 (iq256 rows)"}.get(isa, "scalar") + ", kq256 rows",
+            "threads_note": (f"one worker per physical core of the process mask, pinned, the caller working too; "
+                             f"capped at {CPU_SHARE}, the host share of one GPU on the GPU box"
+                             if topo["mask_physical"] > CPU_SHARE else
+                             "one worker per physical core of the process mask, pinned, the caller working too"),
+            "sample": f"{iters} passes x {layers} layers over {len(runs)} piece(s) of {Tc} token(s), median pass; "
+                      f"reference CPU expert rows, Q8_K activations"
+                      + (f" (the first {sum(r[0] for r in runs)} of the {T}-token chunk)" if T > Tc else "")}
 
 
 def cpu_port(L, per, T, k, shared, seconds):

@@ -89,7 +89,7 @@ def ref() -> C.CDLL:
             "ref_q8k_quant": (None, [P, P, I64]),
             "ref_rows": (I32, [I32, P, I32, I32, P, I32, P]),
             "ref_gu_rows": (I32, [I32, P, I32, I32, P, I32, P]),
-            "ref_moe_decode": (C.c_double, [I32, I32, I32, I32, I32, I32, I32, P, P, P, U64, U64, P, P, P, I32, I32]),
+            "ref_moe_decode": (C.c_double, [I32, I32, I32, I32, I32, I32, I32, P, P, P, U64, U64, P, P, P, I32, I32, P]),
         }
         for name, (res, args) in sig.items():
             f = getattr(h, name)

@@ -85,8 +85,9 @@ void quant_act(int t, const float* x, int n, void* dst) {
 // takes the pointer down before it waits for users_ to reach 0, so no worker touches a finished batch.
 class Pool {
 public:
-    explicit Pool(int n) : n_(n) {
-        for (int i = 1; i < n; ++i) th_.emplace_back([this, i] { loop(i); });
+    // worker i (1..n-1) pinned to cpus[i] when cpus is given, else to logical CPU i
+    Pool(int n, const int32_t* cpus) : n_(n) {
+        for (int i = 1; i < n; ++i) th_.emplace_back([this, i, c = cpus ? cpus[i] : -1] { loop(i, c); });
     }
     ~Pool() {
         quit_.store(true);
@@ -120,10 +121,10 @@ private:
             b.left.fetch_sub(1);
         }
     }
-    void loop(int i) {
+    void loop(int i, int cpu) {
         cpu_set_t s;
         CPU_ZERO(&s);
-        CPU_SET(i % (int) std::thread::hardware_concurrency(), &s);
+        CPU_SET(cpu >= 0 ? cpu : i % (int) std::thread::hardware_concurrency(), &s);
         pthread_setaffinity_np(pthread_self(), sizeof s, &s);
         uint64_t seen = gen_.load();
         while (!quit_.load()) {
@@ -183,8 +184,18 @@ __attribute__((visibility("default"))) double ref_moe_decode(int gu_type, int d_
                                                              int k, int n_layers, const int32_t* ids, const float* wts,
                                                              const uint8_t* blobs, uint64_t stride,
                                                              uint64_t layer_stride, const uint8_t* shared,
-                                                             const float* sgs, float* x, int threads, int iters) {
+                                                             const float* sgs, float* x, int threads, int iters,
+                                                             const int32_t* cpus) {
     if (n_tok < 1 || n_tok > 8 || k < 1 || n_layers < 1) return -1.0;
+    // the calling thread works too: on cpus[0] for the duration of the call (its own mask restored afterwards)
+    cpu_set_t saved;
+    const bool pin_self = cpus != nullptr && sched_getaffinity(0, sizeof saved, &saved) == 0;
+    if (pin_self) {
+        cpu_set_t one;
+        CPU_ZERO(&one);
+        CPU_SET(cpus[0], &one);
+        sched_setaffinity(0, sizeof one, &one);
+    }
     const size_t gu_row = row_bytes(gu_type, n_embd), d_row = row_bytes(d_type, n_ff);
     const size_t up_off = (size_t) n_ff * gu_row, down_off = 2 * up_off;
     const size_t ab = act_bytes(gu_type, n_embd), hb = act_bytes(d_type, n_ff);
@@ -206,7 +217,7 @@ __attribute__((visibility("default"))) double ref_moe_decode(int gu_type, int d_
     }
     std::vector<uint8_t> act((size_t) n_tok * ab), hq((size_t) n_ent * hb);
     std::vector<float> h((size_t) n_ent * n_ff), part((size_t) n_ent * n_embd);
-    Pool pool(threads);
+    Pool pool(threads, cpus);
     constexpr int kGuRows = 32, kDownRows = 64;
     const int gu_tasks = (n_ff + kGuRows - 1) / kGuRows, d_tasks = (n_embd + kDownRows - 1) / kDownRows;
     std::vector<double> times;
@@ -254,6 +265,7 @@ __attribute__((visibility("default"))) double ref_moe_decode(int gu_type, int d_
         }
         times.push_back(std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() / n_layers);
     }
+    if (pin_self) sched_setaffinity(0, sizeof saved, &saved);
     std::sort(times.begin(), times.end());
     return times[times.size() / 2];
 }
