@@ -249,12 +249,13 @@ def test_expert_grouped_grid_groups_invariant():
 @pytest.mark.parametrize("w_cols", [512, 2048])
 @pytest.mark.parametrize("w_rows", [64, 128, 256, 96])
 def test_mmq_run_skewed_groups(t, w_cols, w_rows):
-    """One grouped product over experts with 0, 1, 17, 70 and 130 rows (tile tails, empty experts, several tiles),
+    """One grouped product over experts with 0, 1, 17, 70, 130, 255, 256 and 530 rows (tile tails, empty experts,
+    several tiles, whole tiles, an expert over 500 rows as configs[4]'s Zipf routing makes),
     rows scattered to dst through ids; against the oracle's per-row dot on the same Q8_1 codes.  64, 128 and 256
     weight rows take the MFMA tiles with 2, 4 and 8 waves (512 IQ3 columns: rows that start off 16-byte alignment),
     96 rows the row-dot kernel."""
     rng = np.random.default_rng(t + w_cols + w_rows)
-    counts = [0, 70, 1, 130, 17]
+    counts = [0, 70, 1, 130, 17, 530, 255, 256]
     n, total = len(counts), sum(counts)
     bounds = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     W = [ops.quantize_weights(t, rng.normal(0, 0.02, (w_rows, w_cols)).astype(np.float32)) for _ in range(n)]
@@ -301,7 +302,7 @@ def test_mmq_gate_up_swiglu_matches_the_call_sequence(t, N, FF, gather):
     activation rows are token rows taken through a map (gather) or the sorted rows themselves; and h against the
     oracle's SwiGLU of its own dot products, to the Q8_1 rounding."""
     rng = np.random.default_rng(t * 11 + N + FF + gather)
-    counts = [0, 70, 1, 130, 17]
+    counts = [0, 70, 1, 130, 17, 530, 255, 256]
     n, total = len(counts), sum(counts)
     bounds = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     W = [ops.quantize_weights(t, rng.normal(0, 0.05, (2 * FF, N)).astype(np.float32)) for _ in range(n)]
