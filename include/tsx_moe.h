@@ -142,6 +142,19 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* L, const void* blobs, 
                                  int n_tok, const float* logits, const float* x, const void* shared, const float* sgate,
                                  int sg_stride, float* y, int32_t* ids, float* wts, void* scratch, void* stream);
 
+/* tsx_moe_decode_layer without a scratch argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops that allocate nothing after start-up, harnesses that forbid hipMalloc).  No counterpart
+ * in the reference.  The scratch is a fixed device array of tsx_moe_decode_layer_noalloc_max_bytes() (128 KiB) per
+ * GPU, held until the process ends; its address is looked up once per device (with that device current) on the first
+ * call.  A call needing more scratch than that (tsx_moe_decode_layer_scratch_bytes) returns TSX_ERR_UNSUPPORTED.
+ * Nothing is allocated or freed.  Calls share their GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race; calls in one stream's order do not. */
+TSX_API size_t tsx_moe_decode_layer_noalloc_max_bytes(void);
+TSX_API int tsx_moe_decode_layer_noalloc(const tsx_expert_layout* L, const void* blobs, uint64_t stride, int n_expert,
+                                         int k, int n_tok, const float* logits, const float* x, const void* shared,
+                                         const float* sgate, int sg_stride, float* y, int32_t* ids, float* wts,
+                                         void* stream);
+
 /* ------------------------------------------------------------------------------------------------ routing */
 /* logits [n_tok][n_expert] -> ids [n_tok][k] and weights [n_tok][k]: softmax, k rounds of argmax (ties to the
  * lower id; NaN probabilities never win), weights renormalized by max(sum of the picks, 6.1035e-5).

@@ -168,6 +168,8 @@ SIGNATURES = {
     "tsx_moe_mmvq_slots": (I32, [I32, C.POINTER(MmvqSlots), I32, I32, I32, P]),
     "tsx_moe_decode_layer_scratch_bytes": (SZ, [I32, I32, I64]),
     "tsx_moe_decode_layer": (I32, [C.POINTER(ExpertLayout), P, U64, I32, I32, I32, P, P, P, P, I32, P, P, P, P, P]),
+    "tsx_moe_decode_layer_noalloc_max_bytes": (SZ, []),
+    "tsx_moe_decode_layer_noalloc": (I32, [C.POINTER(ExpertLayout), P, U64, I32, I32, I32, P, P, P, P, I32, P, P, P, P]),
     "tsx_moe_router_topk": (I32, [P, P, P, I32, I32, I32, P]),
     "tsx_moe_group": (I32, [P, I32, I32, I32, P, U64, P, P, P, P, P, P]),
     "tsx_moe_group_resident": (I32, [P, I32, I32, I32, P, P, U64, P, P, P, P, P, P]),

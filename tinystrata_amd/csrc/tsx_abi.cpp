@@ -35,8 +35,13 @@ TSX_API int tsx_moe_abi(void) { return TSX_MOE_ABI_VERSION * 100000 + (int) size
 TSX_API int tsx_moe_init(int device) {
     hipError_t e = hipSetDevice(device);
     if (e == hipSuccess) e = hipFree(nullptr);
-    if (e != hipSuccess) tsx::set_error("tsx_moe_init(%d): %s", device, hipGetErrorString(e));
-    return (int) e;
+    if (e != hipSuccess) {
+        tsx::set_error("tsx_moe_init(%d): %s", device, hipGetErrorString(e));
+        return (int) e;
+    }
+    // the no-allocation decode layer's scratch address on this device, looked up now rather than on its first call
+    if (!tsx::noalloc_scratch_ptr()) return TSX_ERR_ARG;
+    return TSX_OK;
 }
 
 TSX_API const char* tsx_moe_last_error(void) { return tsx::error_cstr(); }

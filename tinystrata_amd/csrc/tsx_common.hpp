@@ -20,6 +20,10 @@ int launch_status(const char* what);
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t) p % a) == 0; }
 
+// The current device's address of the no-allocation decode layer's scratch array (tsx_layer.hip); nullptr, with the
+// error recorded, when the runtime refuses the lookup.
+void* noalloc_scratch_ptr();
+
 #define TSX_REQUIRE(cond, ...)                  \
     do {                                        \
         if (!(cond)) {                          \

@@ -39,6 +39,7 @@
 #include "tsx_device.hpp"
 
 #include <climits>
+#include <mutex>
 #include <type_traits>
 
 namespace tsx {
@@ -566,6 +567,40 @@ size_t set_max_lds(const void* kern) {
     return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int) limit) == hipSuccess ? limit : 0;
 }
 }  // namespace
+
+// The scratch of tsx_moe_decode_layer_noalloc: one copy on every GPU the library runs on, held until the process
+// ends.  Host code never passes this name to a kernel (on the host it is a stand-in, not a device address): it uses
+// the per-device address that hipGetSymbolAddress returned for it.
+constexpr size_t kNoAllocScratchBytes = 128 * 1024;
+static __device__ __align__(256) uint8_t noalloc_scratch[kNoAllocScratchBytes];
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+}  // namespace
+
+// The current device's address of noalloc_scratch (looked up once per device, with that device current); nullptr
+// with the error recorded when the runtime refuses.
+void* noalloc_scratch_ptr() {
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+        set_error("tsx_moe_decode_layer_noalloc: no current device (or one past the first %d)", kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error("tsx_moe_decode_layer_noalloc: hipGetSymbolAddress on device %d: %s", device,
+                      hipGetErrorString(e));
+            return nullptr;
+        }
+        g_noalloc_ptr[device] = p;
+    }
+    return g_noalloc_ptr[device];
+}
+
 }  // namespace tsx
 
 using namespace tsx;
@@ -658,6 +693,27 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
         kern<<<(unsigned) (L.n_embd / kRowsB), kThreadsB, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/down");
     });
+}
+
+TSX_API size_t tsx_moe_decode_layer_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+TSX_API int tsx_moe_decode_layer_noalloc(const tsx_expert_layout* Lp, const void* blobs, uint64_t stride, int n_expert,
+                                         int k, int n_tok, const float* logits, const float* x, const void* shared,
+                                         const float* sgate, int sg_stride, float* y, int32_t* ids, float* wts,
+                                         void* stream) {
+    TSX_REQUIRE(Lp != nullptr, "tsx_moe_decode_layer_noalloc: null layout");
+    const size_t need = tsx_moe_decode_layer_scratch_bytes(n_tok, k, Lp->n_ff);
+    if (need > kNoAllocScratchBytes) {
+        set_error("tsx_moe_decode_layer_noalloc: %d tokens x top-%d at n_ff %lld need %zu scratch bytes, more than the "
+                  "%zu this entry point holds per GPU",
+                  n_tok, k, (long long) Lp->n_ff, need, kNoAllocScratchBytes);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    void* p = noalloc_scratch_ptr();
+    if (!p) return TSX_ERR_ARG;
+    // every word launch B reads of the scratch is written by launch A of the same call first: nothing to clear
+    return tsx_moe_decode_layer(Lp, blobs, stride, n_expert, k, n_tok, logits, x, shared, sgate, sg_stride, y, ids, wts,
+                                p, stream);
 }
 
 }  // extern "C"
