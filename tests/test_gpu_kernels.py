@@ -29,6 +29,28 @@ def test_quantize_q8_1_bytes_exact():
     assert (got == O.quantize_q8_1(x)).all()
 
 
+def test_quantize_q8_1_halves_exact():
+    """Quotients on and next to half-integers, where a quotient one ulp off would change roundf's code: the GPU forms
+    v / d as a corrected product of the reciprocal, which must give the reference's codes (IEEE division, roundf) for
+    every one of them, across block scales from subnormal-adjacent to the fp16 clamp."""
+    rng = np.random.default_rng(11)
+    rows, nb = 4096, 8
+    amax = np.exp(rng.uniform(np.log(1e-36), np.log(1e7), (rows, nb))).astype(np.float32)
+    d = np.minimum(amax / np.float32(127.0), np.float32(65504.0)).astype(np.float32)
+    n = rng.integers(-127, 127, (rows, nb, 31)).astype(np.float32)
+    half = (n + np.float32(0.5)) * d[..., None]
+    nudge = rng.integers(-3, 4, (rows, nb, 31))                    # a few ulps either side of the half
+    vals = np.nextafter(half, np.where(nudge > 0, np.inf, -np.inf)).astype(np.float32)
+    for _ in range(2):
+        vals = np.where(np.abs(nudge) > 1, np.nextafter(vals, np.where(nudge > 0, np.inf, -np.inf)), vals)
+    vals = np.where(nudge == 0, half, vals).astype(np.float32)
+    x = np.concatenate([amax[..., None], vals], axis=2)             # the block's amax first
+    x = np.where(rng.random(x.shape) < 0.5, -x, x).astype(np.float32).reshape(rows, nb * 32)
+    assert np.isfinite(x).all()
+    got = host(ops.quantize_q8_1_rows(dev(x)))
+    assert (got == O.quantize_q8_1(x)).all()
+
+
 @pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("n", [256, 2048])
 def test_subblock_sums_exact(t, n):

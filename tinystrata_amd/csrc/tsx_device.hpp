@@ -128,6 +128,13 @@ __device__ __forceinline__ RepTab<T> rep_store(uint8_t* lds, const uint64_t (&v)
                      (const uint64_t*) (lds + rep_grid_bytes<T>()) + lane % max(rep_sign_copies<T>(), 1)};
 }
 
+// a lane's view of copies stored earlier by rep_store (by whichever threads stored them)
+template <int T>
+__device__ __forceinline__ RepTab<T> rep_view(const uint8_t* lds) {
+    const int lane = __lane_id();
+    return RepTab<T>{(const uint32_t*) lds + lane % max(rep_grid_copies<T>(), 1),
+                     (const uint64_t*) (lds + rep_grid_bytes<T>()) + lane % max(rep_sign_copies<T>(), 1)};
+}
 // table reads, by where the tables are: the constant tables (GridRef) or a lane's copies (RepTab)
 template <int T> __device__ __forceinline__ uint32_t tab_grid(const GridRef& g, uint32_t i) {
     return T == TSX_IQ3_XXS ? g.xxs[i] : g.s[i];
@@ -451,6 +458,24 @@ struct OpAdd {
 // ------------------------------------------------------------------ Q8_1 of 32 values held by 32 lanes
 // lane i (i = lane & 31) holds x; the 32-lane xor tree for amax and for the sum (the order the oracle restates)
 __device__ __forceinline__ float q8_1_finite(float v) { return fabsf(v) > 65504.0f ? copysignf(65504.0f, v) : v; }
+// The Q8_1 code of v in a block of scale d = q8_1_finite(amax / 127) (amax the block's largest magnitude):
+// roundf(v / d) clamped to [-127, 127], 0 when amax is 0 - the reference quantizer's code, bit for bit.  rd = 1 / d is
+// the correctly rounded reciprocal (one IEEE division per block); the quotient is Markstein's corrected product
+// q = v rd, r = v - d q (exact by fma), q + r rd, which is the correctly rounded v / d when rd is and nothing under- or
+// overflows (d >= 2^-100; a smaller d takes the division).  roundf ties away from zero; the clamp is one v_med3.
+__device__ __forceinline__ int q8_1_code_rd(float v, float amax, float d, float rd) {
+    if (amax == 0.0f) return 0;
+    float z;
+    if (d >= 0x1p-100f) {
+        const float q = v * rd;
+        z = __builtin_fmaf(__builtin_fmaf(-d, q, v), rd, q);
+    } else {
+        z = v / d;
+    }
+    const float t = __builtin_truncf(z);
+    const float r = t + (__builtin_fabsf(z - t) >= 0.5f ? __builtin_copysignf(1.0f, z) : 0.0f);
+    return (int) __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
+}
 __device__ __forceinline__ void q8_1_store32(float x, tsx_block_q8_1* y, int i) {
     float amax = fabsf(x), sum = x;
 #pragma unroll
@@ -459,12 +484,7 @@ __device__ __forceinline__ void q8_1_store32(float x, tsx_block_q8_1* y, int i) 
         sum += __shfl_xor(sum, o, 32);
     }
     const float d = q8_1_finite(amax / 127.0f);
-    int8_t q = 0;
-    if (amax != 0.0f) {
-        const float r = roundf(x / d);
-        q = (int8_t) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
-    }
-    y->qs[i] = q;
+    y->qs[i] = (int8_t) q8_1_code_rd(x, amax, d, 1.0f / d);
     if (i == 0) {
         y->d = f2h(q8_1_finite(d));
         y->s = f2h(q8_1_finite(sum));

@@ -60,6 +60,7 @@ constexpr int kRowsB = 8;             // output rows per block of launch B
 constexpr int kSlabB = 64 * 1024;     // most LDS bytes of a chunk of groups' down rows (8 rows of each)
 constexpr int kBLoads = kSlabB / 16 / kThreadsB;  // 16-byte loads per thread in flight: a whole chunk
 constexpr int kHLoads = 3;            // 16-byte pieces of h per thread prefetched by launch B
+constexpr int kItemsB1 = 2;           // launch B at one token: (row, unit) items per thread
 static_assert(kMaxTok <= kThreadsA / 64, "one wave per token in the routing");
 
 // the tables launch A leaves for launch B, at the start of the scratch buffer
@@ -94,6 +95,9 @@ struct LayerArgs {
     LayerTables* tab;
     int8_t* hc;                   // Q8_1 codes of h [P][n_ff], P = n_tok * k (+ n_tok shared): expert order positions
     float* hd;                    // their scales [P][n_ff / 32], right after the codes
+    float* hf;                    // one-token launch A: h in fp32 [P][n_ff] (where hc would be); launch B quantizes it
+    int h_fp32;                   // launch B reads hf instead of hc / hd
+    int rows_w;                   // one-token launch A: rows per wave (the slab holds rows_w rows of each wave)
 };
 
 // one Q8_1 activation unit (32 codes + scale) from LDS planes (codes row-major, one float scale per 32)
@@ -109,22 +113,17 @@ __device__ __forceinline__ void act_planes(const int8_t* codes, const float* d, 
     a.d = *(lds_ptr<const float>) d;
 }
 
-// the Q8_1 code of v in a block whose largest magnitude is amax (scale d = q8_1_finite(amax / 127)): the codes of
-// q8_1_store32, byte for byte
-__device__ __forceinline__ int q8_1_code(float v, float amax, float d) {
-    if (amax == 0.0f) return 0;
-    const float r = roundf(v / d);
-    return (int) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
-}
 
 // Q8_1 of a 32-value block held as 4 floats by each of 8 consecutive lanes (lane l of the block: values 4l..4l+3)
 // into LDS planes.  All 64 lanes of the wave take part.
 __device__ __forceinline__ void q8_1_quad_to_lds(const float4& x, bool valid, int8_t* codes, float* d, int l8) {
     float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
     amax = lanes_reduce<8>(amax, OpMax());
-    const float dd = q8_1_finite(amax / 127.0f);
-    const uint32_t packed = ((uint32_t) q8_1_code(x.x, amax, dd) & 0xFFu) | ((uint32_t) q8_1_code(x.y, amax, dd) & 0xFFu) << 8 |
-                            ((uint32_t) q8_1_code(x.z, amax, dd) & 0xFFu) << 16 | ((uint32_t) q8_1_code(x.w, amax, dd) & 0xFFu) << 24;
+    const float dd = q8_1_finite(amax / 127.0f), rd = 1.0f / dd;
+    const uint32_t packed = ((uint32_t) q8_1_code_rd(x.x, amax, dd, rd) & 0xFFu) |
+                            ((uint32_t) q8_1_code_rd(x.y, amax, dd, rd) & 0xFFu) << 8 |
+                            ((uint32_t) q8_1_code_rd(x.z, amax, dd, rd) & 0xFFu) << 16 |
+                            ((uint32_t) q8_1_code_rd(x.w, amax, dd, rd) & 0xFFu) << 24;
     if (valid) {
         *(uint32_t*) codes = packed;
         if (l8 == 0) *d = h2f(f2h(dd));
@@ -369,12 +368,175 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
             const float dd = q8_1_finite(amax / 127.0f);
             if ((tid >> 5) < n_e) {
                 const int64_t p = p0 + e;
-                a.hc[p * FF + kSliceA * cur.j + i] = (int8_t) q8_1_code(h, amax, dd);
+                a.hc[p * FF + kSliceA * cur.j + i] = (int8_t) q8_1_code_rd(h, amax, dd, 1.0f / dd);
                 if (i == 0) a.hd[p * (FF / 32) + cur.j] = h2f(f2h(dd));
             }
         }
         if (sl + 1 < s1) __syncthreads();  // s_gu is free for the next slice
         cur = nxt;
+    }
+}
+
+// ------------------------------------------------------------------ launch A at one token
+// At one token the slices above (32 gate/up row pairs of one expert: one Q8_1 block of h) number (k + 1) * n_ff / 32,
+// 144 at configs[1], fewer than the 256 CUs, so 112 CUs would idle while the rest decode 64 rows each.  This launch
+// spreads the (k + 1) * n_ff gate/up row pairs evenly over all the blocks instead, in the order [shared expert | pick 0 |
+// pick 1 | ...], and writes h in fp32 (a Q8_1 block of h may straddle two blocks); launch B quantizes it.  A block
+// needs the routing only as far as its last pick: a block of the shared expert issues its row loads at once, the others
+// after as many argmax rounds as their picks need.  Row i of a block (pair i / 2, gate for even i, up for odd) belongs
+// to wave i % 16; the 64 lanes of the wave take the row's units in turn and reduce the row with DPP; SwiGLU pairs the
+// two rows through LDS.  The last block, whose last pick is the k-th, writes the tables launch B reads.
+constexpr int kPiecesRow1 = 3;        // 16-byte loads per lane and row (rows of at most 3 KB)
+constexpr int kMaxRowsW1 = 4;         // rows per wave
+template <int GT>
+__global__ void __launch_bounds__(kThreadsA) layer_gu1_kernel(LayerArgs a) {
+#pragma clang fp contract(off)
+    constexpr int RPH = (rep_stores<GT>() + kThreadsA - 1) / kThreadsA;
+    using Tab = std::conditional_t<(RPH > 0), RepTab<GT>, GridRef>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int32_t s_pick[16];
+    __shared__ float s_pw[16];
+    __shared__ float s_row[kWavesA * kMaxRowsW1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int k = a.k;
+    const tsx_expert_layout L = a.L;
+    const int N = (int) L.n_embd, NU = N / 32, FF = (int) L.n_ff;
+    const int sh = a.shared ? 1 : 0;
+    const int P = (k + sh) * FF;  // row pairs: [shared | pick 0 | ... | pick k-1]
+    const int nb = (int) gridDim.x, b = (int) blockIdx.x;
+    const int p0 = (int) ((int64_t) b * P / nb), p1 = (int) ((int64_t) (b + 1) * P / nb);
+    const int nrows = 2 * (p1 - p0);
+    const int rounds = max(0, (p1 - 1) / FF + 1 - sh);  // the picks this block's pairs reach
+
+    // 0. the routing wave's logits first, then the codebooks and, by the other waves, the activations
+    float lg[kRouteV];
+    if (wave == 0 && rounds > 0) route_fetch(a.logits, a.n_expert, lane, lg);
+    uint64_t rv[RPH > 0 ? RPH : 1];
+    if constexpr (RPH > 0) rep_fetch<GT, RPH>(rv, tid, kThreadsA);
+    const int nq_all = N / 4, xt = tid - 64, nxt = kThreadsA - 64;
+    const float4* x4 = (const float4*) a.x;
+    float4 xv[kXLoads];
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(max(xt, 0) + nxt * i, nq_all - 1)];
+    // the row loads below must not be issued ahead of these: a wait for these would then wait for the rows too
+    __builtin_amdgcn_sched_barrier(0);
+    const int rows_w = a.rows_w;
+    const uint64_t gu_row = L.gu_row;
+    const int ppr = (int) (gu_row / 16);  // 16-byte pieces per row
+    const int cpr = (ppr + 63) / 64;      // loads per lane and row
+    const int my_rows = wave < nrows ? (nrows - 1 - wave) / kWavesA + 1 : 0;  // rows wave, wave + 16, ...
+    v4i* wslab = (v4i*) smem + wave * (rows_w * ppr);
+    int8_t* s_xq = (int8_t*) (smem + (size_t) kWavesA * rows_w * gu_row + rep_lds_bytes<GT>());
+    float* s_xd = (float*) (s_xq + N);
+
+    // the rest for the wave's row count as straight-line code: the loads of all its rows in flight together, and
+    // every row's unit decode independent of the others', so all their codebook lookups are in flight at once
+    auto body = [&](auto RC) {
+        constexpr int R = decltype(RC)::value;
+        v4i reg[R > 0 ? R : 1][kPiecesRow1];
+        // row j of the wave (block row wave + 16 j): pair p0 + i / 2, gate rows for even i, up rows for odd; the
+        // address is the same in every lane
+        auto row_base = [&](int j) -> uintptr_t {
+            const int i = wave + kWavesA * j, pr = p0 + i / 2, slot = pr / FF, r = pr - slot * FF;
+            const uint8_t* blob = slot < sh ? a.shared : a.blobs + (uint64_t) s_pick[slot - sh] * a.stride;
+            return (uintptr_t) (blob + ((i & 1) ? L.up_off : 0) + (uint64_t) r * gu_row);
+        };
+        auto issue = [&]() {
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const gbl_ptr<const v4i> src = gbl_at<v4i>(row_base(j));
+#pragma unroll
+                for (int c = 0; c < kPiecesRow1; ++c)
+                    if (c < cpr) reg[j][c] = __builtin_nontemporal_load(src + min(lane + 64 * c, ppr - 1));
+            }
+        };
+        // a block of the shared expert alone needs no routing: its rows are requested before anything else waits
+        if (R > 0 && rounds == 0) issue();
+        __builtin_amdgcn_sched_barrier(0);
+
+        // 1. routing (wave 0, as many rounds as the block's picks need) while the other waves quantize x into LDS
+        if (wave == 0) {
+            if (rounds > 0) route_select(lg, a.n_expert, rounds, lane, s_pick, s_pw);
+        } else {
+            for (int base = 0; base < nq_all; base += nxt * kXLoads) {
+                if (base > 0) {
+#pragma unroll
+                    for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(base + xt + nxt * i, nq_all - 1)];
+                }
+#pragma unroll
+                for (int i = 0; i < kXLoads; ++i) {
+                    const int qd = base + xt + nxt * i;
+                    if (base + nxt * i < nq_all)  // the same for every thread of these waves
+                        q8_1_quad_to_lds(xv[i], qd < nq_all, s_xq + 4 * qd, s_xd + qd / 8, xt & 7);
+                }
+            }
+        }
+        Tab grid;
+        if constexpr (RPH > 0) {
+            uint8_t* tabs = smem + (size_t) kWavesA * rows_w * gu_row;
+            rep_store<GT, RPH>(tabs, rv, tid, kThreadsA);
+            grid = rep_view<GT>(tabs);
+        } else {
+            grid = grid_const();
+        }
+        __syncthreads();  // picks, activations and codebooks are in LDS
+        if (R > 0 && rounds > 0) issue();
+        __builtin_amdgcn_sched_barrier(0);
+        if (rounds == k && b == nb - 1) {  // the tables launch B reads: group g = pick g, entry g, position g
+            if (tid < k) {
+                a.ids[tid] = s_pick[tid];
+                a.wts[tid] = s_pw[tid];
+                a.tab->wts[tid] = s_pw[tid];
+                a.tab->ent_pos[tid] = tid;
+                a.tab->grp_expert[tid] = s_pick[tid];
+            }
+            if (tid <= k) a.tab->grp_start[tid] = tid;
+            if (tid == 0) a.tab->n_groups = k;
+        }
+        if constexpr (R > 0) {
+            // 2. the rows into the wave's slab, then each row's dot with x, the 64 lanes reduced with DPP
+#pragma unroll
+            for (int j = 0; j < R; ++j)
+#pragma unroll
+                for (int c = 0; c < kPiecesRow1; ++c)
+                    if (c < cpr && lane + 64 * c < ppr) wslab[j * ppr + lane + 64 * c] = reg[j][c];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's LDS writes land before its reads
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            float acc[R] = {};
+            for (int u = lane; u < NU; u += 64) {
+                Act xa;
+                act_planes(s_xq + 32 * u, s_xd + u, xa);
+                Unit w[R];
+#pragma unroll
+                for (int j = 0; j < R; ++j) unit_load<GT>((const uint8_t*) (wslab + j * ppr), u, w[j], grid);
+#pragma unroll
+                for (int j = 0; j < R; ++j) {
+                    int S, M;
+                    acc[j] += unit_dot<GT>(w[j], xa, S, M);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                const float v = lanes_sum<64>(acc[j]);
+                if (lane == 0) s_row[wave + kWavesA * j] = v;
+            }
+        }
+        __syncthreads();
+    };
+    switch (my_rows) {  // the same in every lane of the wave; every case holds the same two block barriers
+        case 0: body(std::integral_constant<int, 0>{}); break;
+        case 1: body(std::integral_constant<int, 1>{}); break;
+        case 2: body(std::integral_constant<int, 2>{}); break;
+        case 3: body(std::integral_constant<int, 3>{}); break;
+        default: body(std::integral_constant<int, 4>{}); break;
+    }
+    // 3. h = silu(gate) * up per pair (the product rounded on its own), in fp32 at its position: pick j -> j, shared -> k
+    for (int i = tid; 2 * i < nrows; i += kThreadsA) {
+        const int pr = p0 + i, slot = pr / FF, r = pr - slot * FF;
+        const int pos = slot < sh ? k : slot - sh;
+        const float gt = s_row[2 * i];
+        a.hf[(int64_t) pos * FF + r] = (gt / (1.0f + expf(-gt))) * s_row[2 * i + 1];
     }
 }
 
@@ -408,8 +570,9 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     uint64_t rv[RP > 0 ? RP : 1];
     if constexpr (RP > 0) rep_fetch<DT, RP>(rv, tid, kThreadsB);
     const int P = n_ent + (a.shared ? T : 0);
-    const int nh = (P * FF + P * NUd * 4) / 16;  // 16-byte pieces (n_ff is a multiple of 128)
-    const v4i* hsrc = (const v4i*) a.hc;
+    // h: the Q8_1 planes (16-byte pieces; n_ff is a multiple of 128), or fp32 h (float4 quads) quantized here
+    const int nh = a.h_fp32 ? P * FF / 4 : (P * FF + P * NUd * 4) / 16;
+    const v4i* hsrc = (const v4i*) (a.h_fp32 ? (const void*) a.hf : (const void*) a.hc);
     v4i hv[kHLoads];
 #pragma unroll
     for (int i = 0; i < kHLoads; ++i) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
@@ -430,26 +593,44 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     // the groups' rows in chunks of gpc groups, every piece of a chunk in flight at once
     const int gb = (int) (kRowsB * d_row), ppg = gb / 16;  // bytes and 16-byte pieces of a group's 8 rows
     const int gpc = max(1, a.slab_b / gb), nchunks = (G + gpc - 1) / gpc;
+    const float rppg = __builtin_amdgcn_rcpf((float) ppg);
     v4i reg[kBLoads];
     auto issue = [&](int ch) {
         const int g0 = ch * gpc, np = min(gpc, G - g0) * ppg;
 #pragma unroll
         for (int i = 0; i < kBLoads; ++i) {  // unconditional (clamped) loads keep the wait counts exact
-            const int q = min(tid + kThreadsB * i, np - 1), g = q / ppg, pp = q - g * ppg;
+            const int q = min(tid + kThreadsB * i, np - 1), g = div_small(q, ppg, rppg), pp = q - g * ppg;
             reg[i] = __builtin_nontemporal_load(gbl_at<v4i>((uintptr_t) s_gsrc[g0 + g]) + pp);
         }
     };
     issue(0);
+    // the row loads stay here, ahead of the work below (the compiler would otherwise sink them towards their use)
+    __builtin_amdgcn_sched_barrier(0);
 
     // h into LDS: the prefetched pieces, then any rest
     if (tid < T) s_sgate[tid] = sg;
     int8_t* s_hq = (int8_t*) (smem + a.slab_b + rep_lds_bytes<DT>());
     float* s_hd = (float*) (s_hq + (size_t) P * FF);
-    v4i* hdst = (v4i*) s_hq;
+    if (a.h_fp32) {  // every Q8_1 block of h from its eight quads (consecutive lanes), as launch A would write it
+        // (the loop conditions are the same in every thread: whole waves take part in each block's reduction)
 #pragma unroll
-    for (int i = 0; i < kHLoads; ++i)
-        if (tid + kThreadsB * i < nh) hdst[tid + kThreadsB * i] = hv[i];
-    for (int idx = tid + kThreadsB * kHLoads; idx < nh; idx += kThreadsB) hdst[idx] = hsrc[idx];
+        for (int i = 0; i < kHLoads; ++i) {
+            const int q = tid + kThreadsB * i;
+            if (kThreadsB * i < nh)
+                q8_1_quad_to_lds(__builtin_bit_cast(float4, hv[i]), q < nh, s_hq + 4 * q, s_hd + q / 8, tid & 7);
+        }
+        for (int base = kThreadsB * kHLoads; base < nh; base += kThreadsB) {
+            const int q = base + tid;
+            q8_1_quad_to_lds(__builtin_bit_cast(float4, hsrc[min(q, nh - 1)]), q < nh, s_hq + 4 * q, s_hd + q / 8,
+                             tid & 7);
+        }
+    } else {
+        v4i* hdst = (v4i*) s_hq;
+#pragma unroll
+        for (int i = 0; i < kHLoads; ++i)
+            if (tid + kThreadsB * i < nh) hdst[tid + kThreadsB * i] = hv[i];
+        for (int idx = tid + kThreadsB * kHLoads; idx < nh; idx += kThreadsB) hdst[idx] = hsrc[idx];
+    }
     Tab grid;
     if constexpr (RP > 0) grid = rep_store<DT, RP>(smem + a.slab_b, rv, tid, kThreadsB);
     else grid = grid_const();
@@ -466,9 +647,47 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
         }
         __syncthreads();  // the chunk (and h, the codebooks) are in LDS
         if (ch + 1 < nchunks) issue(ch + 1);
+        const int R = gn * kRowsB;
+        if (a.h_fp32 && (NUd == 8 || NUd == 16 || NUd == 32) && R * NUd <= kItemsB1 * kThreadsB) {
+            // one token: every group has one entry (position grp_lo).  The items (row, unit) go to consecutive
+            // threads, a row's NUd units to NUd lanes of one wave; a thread's items are decoded together (their
+            // codebook lookups in flight at once), then each row is reduced over its lanes with DPP
+            const int items = R * NUd, lgu = NUd == 8 ? 3 : NUd == 16 ? 4 : 5;
+            float v[kItemsB1];
+            int pos[kItemsB1], rr[kItemsB1];
+            Unit w[kItemsB1];
+#pragma unroll
+            for (int m = 0; m < kItemsB1; ++m) {
+                const int it = min(tid + kThreadsB * m, items - 1), ri = it >> lgu, u = it & (NUd - 1);
+                const int g = ri / kRowsB;
+                rr[m] = ri % kRowsB;
+                pos[m] = grp_lo(g0 + g);
+                v[m] = 0.f;
+                if (kThreadsB * m < items)  // the same in every thread
+                    unit_load<DT>((const uint8_t*) smem + g * gb + rr[m] * d_row, u, w[m], grid);
+            }
+#pragma unroll
+            for (int m = 0; m < kItemsB1; ++m) {
+                if (kThreadsB * m < items) {
+                    const int it = min(tid + kThreadsB * m, items - 1), u = it & (NUd - 1);
+                    Act xa;
+                    act_planes(s_hq + (size_t) pos[m] * FF + 32 * u, s_hd + pos[m] * NUd + u, xa);
+                    int S, M;
+                    v[m] = unit_dot<DT>(w[m], xa, S, M);
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < kItemsB1; ++m) {
+                if (kThreadsB * m < items) {
+                    const float t = NUd == 8 ? lanes_sum<8>(v[m]) : NUd == 16 ? lanes_sum<16>(v[m]) : lanes_sum<32>(v[m]);
+                    if ((tid & (NUd - 1)) == 0 && tid + kThreadsB * m < items) s_part[pos[m]][rr[m]] = t;
+                }
+            }
+            __syncthreads();  // the chunk's rows are done before the next chunk overwrites the slab
+            continue;
+        }
         // rows ri = g * 8 + r of the chunk, tpr lanes each (consecutive lanes; tpr divides 64), in passes of
         // kThreadsB / tpr rows when the chunk has more
-        const int R = gn * kRowsB;
         int tpr = 64;
         while (tpr > 4 && R * tpr > kThreadsB) tpr >>= 1;
         const int l = tid % tpr;
@@ -609,7 +828,9 @@ extern "C" {
 
 TSX_API size_t tsx_moe_decode_layer_scratch_bytes(int n_tok, int k, int64_t n_ff) {
     if (n_tok < 1 || k < 1 || n_ff <= 0 || n_ff % 32 != 0) return 0;
-    return kTablesBytes + ((h_bytes(n_tok, k, n_ff) + 255) & ~(size_t) 255);
+    // h as Q8_1 planes, or (one token) in fp32: k routed positions and the shared one
+    const size_t h = std::max(h_bytes(n_tok, k, n_ff), n_tok == 1 ? (size_t) (k + 1) * (size_t) n_ff * 4 : 0);
+    return kTablesBytes + ((h + 255) & ~(size_t) 255);
 }
 
 TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t stride, int n_expert, int k,
@@ -677,15 +898,40 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
     const int P = n_tok * k + (shared ? n_tok : 0);  // h is packed for the positions this call uses
     a.hc = (int8_t*) ((uint8_t*) scratch + kTablesBytes);
     a.hd = (float*) (a.hc + (size_t) P * L.n_ff);
+    a.hf = (float*) a.hc;
+    a.h_fp32 = 0;
+    a.rows_w = 0;
     const hipStream_t s = (hipStream_t) stream;
-    int rc = with_type(L.gu_type, [&](auto T) {
-        auto kern = layer_gu_kernel<decltype(T)::value>;
-        const size_t lds = (size_t) slab_a + fixed_a;
-        // as many blocks as the routing could give slices, at most one per CU
-        const int most = (std::min(n_tok * k, n_expert) + (shared ? 1 : 0)) * (int) (L.n_ff / kSliceA);
-        kern<<<std::min(kBlocksA, most), kThreadsA, lds, s>>>(a);
-        return launch_status("tsx_moe_decode_layer/gate-up");
-    });
+    // one token: the row pairs spread over every CU (launch B quantizes the fp32 h) when the rows tile the slab
+    int rc = TSX_ERR_UNSUPPORTED;
+    if (n_tok == 1 && L.gu_row % 16 == 0) {
+        const int pairs = (k + (shared ? 1 : 0)) * (int) L.n_ff, nb = std::min(kBlocksA, pairs);
+        const int rows = 2 * ((pairs + nb - 1) / nb), rows_w = (rows + kWavesA - 1) / kWavesA;
+        size_t lim1 = 0;
+        with_type(L.gu_type, [&](auto T) {
+            static const size_t limit = set_max_lds((const void*) layer_gu1_kernel<decltype(T)::value>);
+            lim1 = limit;
+            return 0;
+        });
+        const size_t lds1 = (size_t) kWavesA * rows_w * L.gu_row + rep_bytes(L.gu_type) + x_planes_bytes(L, 1);
+        if (rows_w <= kMaxRowsW1 && L.gu_row <= (uint64_t) 64 * kPiecesRow1 * 16 && lds1 <= lim1) {
+            a.h_fp32 = 1;
+            a.rows_w = rows_w;
+            rc = with_type(L.gu_type, [&](auto T) {
+                layer_gu1_kernel<decltype(T)::value><<<nb, kThreadsA, lds1, s>>>(a);
+                return launch_status("tsx_moe_decode_layer/gate-up");
+            });
+        }
+    }
+    if (!a.h_fp32)
+        rc = with_type(L.gu_type, [&](auto T) {
+            auto kern = layer_gu_kernel<decltype(T)::value>;
+            const size_t lds = (size_t) slab_a + fixed_a;
+            // as many blocks as the routing could give slices, at most one per CU
+            const int most = (std::min(n_tok * k, n_expert) + (shared ? 1 : 0)) * (int) (L.n_ff / kSliceA);
+            kern<<<std::min(kBlocksA, most), kThreadsA, lds, s>>>(a);
+            return launch_status("tsx_moe_decode_layer/gate-up");
+        });
     if (rc != TSX_OK) return rc;
     return with_type(L.d_type, [&](auto T) {
         auto kern = layer_down_kernel<decltype(T)::value>;

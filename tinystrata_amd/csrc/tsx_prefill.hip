@@ -73,12 +73,8 @@ __global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __r
     const float4 v = *(const float4*) (x + src * ld + 4 * c4);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = lanes_reduce<8>(amax, OpMax());
-    const float d = q8_1_finite(amax / 127.0f);
-    auto code = [&](float f) {
-        if (amax == 0.0f) return 0;
-        const float r = roundf(f / d);
-        return (int) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
-    };
+    const float d = q8_1_finite(amax / 127.0f), rd = 1.0f / d;
+    auto code = [&](float f) { return q8_1_code_rd(f, amax, d, rd); };
     const int q0 = code(v.x), q1 = code(v.y), q2 = code(v.z), q3 = code(v.w);
     const float qs = lanes_reduce<8>((float) (q0 + q1 + q2 + q3), OpAddF());  // |sum| <= 32 * 127: exact in fp32
     if (valid) {
@@ -111,11 +107,7 @@ __global__ void __launch_bounds__(kThreads) mmq_quantize1_kernel(const float* __
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
     const float d = q8_1_finite(amax / 127.0f);
-    int q = 0;
-    if (amax != 0.0f) {
-        const float r = roundf(v / d);
-        q = (int) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
-    }
+    const int q = q8_1_code_rd(v, amax, d, 1.0f / d);
     int qs = q;
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) qs += __shfl_xor(qs, o, 32);
@@ -708,17 +700,10 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     }
                     float amax = fmaxf(fmaxf(fabsf(hv[0]), fabsf(hv[1])), fmaxf(fabsf(hv[2]), fabsf(hv[3])));
                     amax = lanes_reduce<8>(amax, OpMax());
-                    const float d = q8_1_finite(amax / 127.0f);
+                    const float d = q8_1_finite(amax / 127.0f), rd = 1.0f / d;
                     int qv[4];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        int v = 0;
-                        if (amax != 0.0f) {
-                            const float r = roundf(hv[k] / d);
-                            v = (int) (r > 127.0f ? 127.0f : r < -127.0f ? -127.0f : r);
-                        }
-                        qv[k] = v;
-                    }
+                    for (int k = 0; k < 4; ++k) qv[k] = q8_1_code_rd(hv[k], amax, d, rd);
                     const float qs = lanes_reduce<8>((float) (qv[0] + qv[1] + qv[2] + qv[3]), OpAddF());
                     if (t0 + tok < nrows) {
                         const int64_t hr = row0 + t0 + tok, col = (int64_t) (BM / 2) * bx + 4 * f4;
