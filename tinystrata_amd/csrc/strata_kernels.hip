@@ -169,6 +169,22 @@ void quantize(const float* x, const int32_t* ids, void* xq, int t, int64_t cols,
     check_exit(tsx_moe_mmq_quantize(x, ids, xq, t, cols, ld, rows, stream), "prefill mmq: quantize");
 }
 
+Nvfp4Mode nvfp4_mode() { return Nvfp4Mode::W4A8; }
+bool fp4_activations(int) { return false; }
+
+void scale_gu_rows(float*, int64_t, int64_t, const int32_t*, int, const float*, int64_t, int64_t, void*) {
+    std::fprintf(stderr, "prefill mmq: NVFP4 expert scales are not on this path\n");
+    std::exit(1);
+}
+
+void scale_down_rows(float*, int64_t, const int32_t*, int, const float*, int64_t, void*) {
+    std::fprintf(stderr, "prefill mmq: NVFP4 expert scales are not on this path\n");
+    std::exit(1);
+}
+
+Context::Context() = default;
+Context::~Context() = default;
+
 void Context::run(const Product& p, void* stream) {
     if (p.n <= 0) return;
     if (p.y_scale != nullptr) {
