@@ -73,6 +73,8 @@ def parse_args(argv=None):
     ap.add_argument("--config", default="decode", choices=sorted(CONFIGS))
     ap.add_argument("--eager", action="store_true", help="launch each step eagerly instead of replaying a HIP graph")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--norm", action="store_true",
+                    help="end every layer with the MoE block's norm epilogue (h = rms(x) * norm_w and its Q8_1 image)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prompt-chunk configurations measured after the default decode line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -169,11 +171,17 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None):
     logits_d = torch.from_numpy(logits).to(dev)
     sg_d = torch.from_numpy(sg).to(dev)
     mls = [moe.MoELayer(Ws[l], k, T, dev) for l in range(layers)]
+    # --norm: every layer ends as the reference's MoE block does (k_moe_out_small with the next layer's norm weights):
+    # h = rms(x) * norm_w and its Q8_1 image, the next layer's input
+    norm = {}
+    if args.norm:
+        norm = dict(norm_w=torch.from_numpy((1.0 + 0.1 * rng.normal(0, 1, N)).astype(np.float32)).to(dev), eps=1e-6,
+                    h=torch.empty((T, N), device=dev), hq=torch.empty((T, N // 32 * 36), dtype=torch.uint8, device=dev))
 
     def step():
         x.copy_(x0_d)
         for l in range(layers):
-            mls[l](x, logits_d[l], sg_d[l] if shared else None, x)
+            mls[l](x, logits_d[l], sg_d[l] if shared else None, x, **norm)
 
     for _ in range(warmup):
         step()

@@ -138,6 +138,16 @@ TSX_API int tsx_moe_mmvq_slots(int type, const tsx_mmvq_slots* a, int count, int
  * expert's mmvq / SwiGLU / mmvq (q36_engine.cu:2906-2913) and k_moe_out_small without the norm
  * (q36_kernels.cuh:248-290). */
 TSX_API size_t tsx_moe_decode_layer_scratch_bytes(int n_tok, int k, int64_t n_ff);
+/* tsx_moe_decode_layer with the MoE block's end as k_moe_out_small has it (src/qwen35/q36_kernels.cuh:248-290):
+ * after y[t] is formed, h[t][i] = (y[t][i] * r) * norm_w[i] with r = 1 / sqrt(mean over i of y[t][i]^2 + eps) (the
+ * next layer's attention norm; two roundings, no fma) into h [n_tok][n_embd] (fp32), and, when hq is not null, its
+ * Q8_1 image [n_tok][n_embd / 32] (the next layer's input: the bytes tsx_moe_quantize_q8_1 would write from h).
+ * The norm is a third launch of one workgroup per token.  Same limits and scratch as tsx_moe_decode_layer; n_embd a
+ * multiple of 32. */
+TSX_API int tsx_moe_decode_layer_norm(const tsx_expert_layout* L, const void* blobs, uint64_t stride, int n_expert,
+                                      int k, int n_tok, const float* logits, const float* x, const void* shared,
+                                      const float* sgate, int sg_stride, float* y, int32_t* ids, float* wts,
+                                      const float* norm_w, float eps, float* h, void* hq, void* scratch, void* stream);
 TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* L, const void* blobs, uint64_t stride, int n_expert, int k,
                                  int n_tok, const float* logits, const float* x, const void* shared, const float* sgate,
                                  int sg_stride, float* y, int32_t* ids, float* wts, void* scratch, void* stream);
@@ -194,6 +204,13 @@ TSX_API int tsx_moe_route_sort(const int32_t* ids, int n_ent, int k, int n_exper
  * src/qwen35/q36_kernels.cuh:248-290). */
 TSX_API int tsx_moe_combine(float* x, const float* parts, const int32_t* prow, const float* wts, int k,
                             const float* shared, const float* sgate, int sg_stride, int n, int n_tok, void* stream);
+/* tsx_moe_combine (the same x bits), then h[t] = (x[t] * r) * norm_w with r = 1 / sqrt(mean(x[t]^2) + eps) into
+ * h [n_tok][n] and, when hq is not null, its Q8_1 image [n_tok][n / 32]: the whole of k_moe_out / k_moe_out_small
+ * with the norm (src/qwen35/q36_engine.cu:304-332; src/qwen35/q36_kernels.cuh:248-290).  k 1..16, n a multiple of 32
+ * up to 16384.  One workgroup per token. */
+TSX_API int tsx_moe_combine_norm(float* x, const float* parts, const int32_t* prow, const float* wts, int k,
+                                 const float* shared, const float* sgate, int sg_stride, int n, int n_tok,
+                                 const float* norm_w, float eps, float* h, void* hq, void* stream);
 
 /* ------------------------------------------------------------------------------------------------ prefill */
 /* Bytes of `rows` activation rows of `cols` values quantized for tsx_moe_mmq_run.

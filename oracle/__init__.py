@@ -227,6 +227,13 @@ def combine(x: np.ndarray, parts: np.ndarray, wts: np.ndarray, k: int, prow=None
     return x
 
 
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """The MoE block's norm in closed form (float64): h[t] = x[t] / sqrt(mean(x[t]^2) + eps) * w
+    (src/qwen35/q36_kernels.cuh:276-289; src/qwen35/q36_engine.cu:326-331)."""
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt((x * x).mean(axis=1, keepdims=True) + eps) * np.asarray(w, np.float64)[None, :]
+
+
 # ------------------------------------------------------------------ grouped experts and the layer
 def expert_gu(L: Layout, blobs: list, grp_start: np.ndarray, ent_tok: np.ndarray, xq: np.ndarray):
     """-> h float32 [n_ent, n_ff], hq uint8 [n_ent, n_ff/32*36] (the gate/up half of native_expert_grouped)."""

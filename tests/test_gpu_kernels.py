@@ -184,6 +184,35 @@ def test_mmq_quantize_planes_exact(pad, rows):
     assert (q[rows:] == 0).all() and (d[rows:] == 0).all() and (m[rows:] == 0).all()
 
 
+@pytest.mark.parametrize("shared,prow,n", [(False, False, 2048), (True, True, 2048), (True, False, 4096),
+                                           (False, True, 96)])
+def test_combine_norm(shared, prow, n):
+    """tsx_moe_combine_norm: x is tsx_moe_combine's x bit for bit; h the closed-form norm of it (within float32
+    rounding); hq the Q8_1 image of h byte for byte."""
+    rng = np.random.default_rng(n + shared)
+    T, k, eps = 37, 8, 1e-5
+    parts = rng.normal(0, 1, (T * k, n)).astype(np.float32)
+    wts = rng.random((T, k)).astype(np.float32)
+    x = rng.normal(0, 1, (T, n)).astype(np.float32)
+    x[3] = 0.0                                                   # a row whose only content is the combine
+    pr = dev(rng.permutation(T * k).astype(np.int32)) if prow else None
+    sh = dev(rng.normal(0, 1, (T, n)).astype(np.float32)) if shared else None
+    sg = dev(rng.normal(0, 1, T).astype(np.float32)) if shared else None
+    wn = (1.0 + 0.1 * rng.normal(0, 1, n)).astype(np.float32)
+    pd, wd = dev(parts), dev(wts)
+    x_plain = dev(x)
+    ops.moe_combine(x_plain, pd, wd, k, prow=pr, shared=sh, sgate=sg)
+    xd = dev(x)
+    h = torch.full((T, n), float("nan"), device="cuda")
+    hq = torch.zeros((T, n // 32 * 36), dtype=torch.uint8, device="cuda")
+    ops.moe_combine_norm(xd, pd, wd, k, dev(wn), eps, h, hq, prow=pr, shared=sh, sgate=sg)
+    xv, hv = host(xd), host(h)
+    assert (xv == host(x_plain)).all()
+    ref = O.rms_norm(xv, wn, eps)
+    assert np.abs(hv - ref).max() / np.abs(ref).max() < 2e-6
+    assert (host(hq) == O.quantize_q8_1(hv)).all()
+
+
 # ------------------------------------------------------------------ grouped experts
 CASES = {
     "iq3_2048x512": (IQ3_XXS, IQ3_S, 2048, 512),

@@ -210,3 +210,41 @@ def test_decode_layer_matches_kernel_by_kernel():
     b, ib = run_layer(W, k, x, logits, sgate, fused=False)
     assert (ia == ib).all()
     assert rel_l2(a, b) < 1e-5
+
+
+NORM_CASES = [("c2_decode_iq3", True), ("c3_verify_iq3", True), ("c2_decode_iq3", False), ("c1_decode_q8_0", True),
+              ("c5_prefill_iq3_16tok", True)]
+
+
+@pytest.mark.parametrize("cfg,fused", NORM_CASES,
+                         ids=[f"{c}-{'two_launch' if f else 'kernel_by_kernel'}" for c, f in NORM_CASES])
+def test_moe_block_norm(cfg, fused):
+    """The MoE block's end (k_moe_out_small with the norm): y is bit for bit the layer's y without the norm; h is the
+    closed-form norm of that y (float64 oracle, within float32 rounding); hq is the Q8_1 image of h byte for byte.
+    Three calls in a row give the same bits (the second launch's completion count starts from zero every call)."""
+    gu, d, N, FF, E, k, shared, T = CONFIGS[cfg]
+    L, p, order, W = make_layer(gu, d, N, FF, E, shared)
+    x, logits, sgate = inputs(cfg, T, E, N, seed=len(cfg) + 5)
+    rng = np.random.default_rng(9)
+    wn = (1.0 + 0.1 * rng.normal(0, 1, N)).astype(np.float32)
+    eps = 1e-6
+    layer = moe.MoELayer(W, k, T, torch.device("cuda"), fused=fused)
+    xd, ld, sd, wd = dev(x), dev(logits), dev(sgate) if shared else None, dev(wn)
+    y_plain = torch.zeros((T, N), device="cuda")
+    layer(xd, ld, sd, y_plain)
+    outs = []
+    for _ in range(3):
+        y = torch.zeros((T, N), device="cuda")
+        h = torch.full((T, N), float("nan"), device="cuda")
+        hq = torch.zeros((T, N // 32 * 36), dtype=torch.uint8, device="cuda")
+        layer(xd, ld, sd, y, norm_w=wd, eps=eps, h=h, hq=hq)
+        outs.append((host(y), host(h), host(hq)))
+    yp = host(y_plain)
+    for yv, hv, hqv in outs:
+        assert (yv == yp).all() and (hv == outs[0][1]).all() and (hqv == outs[0][2]).all()
+    yv, hv, hqv = outs[0]
+    ref = O.rms_norm(yv, wn, eps)
+    err = np.abs(hv - ref).max() / np.abs(ref).max()
+    print(f"{cfg}: h against the closed-form norm: max error {err:.2e} of max |h|")
+    assert err < 2e-6
+    assert (hqv == O.quantize_q8_1(hv)).all()

@@ -168,6 +168,8 @@ SIGNATURES = {
     "tsx_moe_mmvq_slots": (I32, [I32, C.POINTER(MmvqSlots), I32, I32, I32, P]),
     "tsx_moe_decode_layer_scratch_bytes": (SZ, [I32, I32, I64]),
     "tsx_moe_decode_layer": (I32, [C.POINTER(ExpertLayout), P, U64, I32, I32, I32, P, P, P, P, I32, P, P, P, P, P]),
+    "tsx_moe_decode_layer_norm": (I32, [C.POINTER(ExpertLayout), P, U64, I32, I32, I32, P, P, P, P, I32, P, P, P, P,
+                                        C.c_float, P, P, P, P]),
     "tsx_moe_decode_layer_noalloc_max_bytes": (SZ, []),
     "tsx_moe_decode_layer_noalloc": (I32, [C.POINTER(ExpertLayout), P, U64, I32, I32, I32, P, P, P, P, I32, P, P, P, P]),
     "tsx_moe_router_topk": (I32, [P, P, P, I32, I32, I32, P]),
@@ -176,6 +178,7 @@ SIGNATURES = {
     "tsx_moe_merge_rows": (I32, [P, P, P, I32, I64, P]),
     "tsx_moe_route_sort": (I32, [P, I32, I32, I32, P, P, P, P, P, P]),
     "tsx_moe_combine": (I32, [P, P, P, P, I32, P, P, I32, I32, I32, P]),
+    "tsx_moe_combine_norm": (I32, [P, P, P, P, I32, P, P, I32, I32, I32, P, C.c_float, P, P, P]),
     "tsx_moe_mmq_q8_bytes": (SZ, [I64, I64]),
     "tsx_moe_mmq_quantize": (I32, [P, P, P, I32, I64, I64, I64, P]),
     "tsx_moe_mmq_run": (I32, [C.POINTER(MmqProduct), P]),

@@ -183,7 +183,7 @@ void scale_down_rows(float*, int64_t, const int32_t*, int, const float*, int64_t
 }
 
 Context::Context() = default;
-Context::~Context() = default;
+Context::~Context() { (void) ctx_; }
 
 void Context::run(const Product& p, void* stream) {
     if (p.n <= 0) return;

@@ -205,7 +205,7 @@ public:
     void run(const Product& p, void* stream);
 
 private:
-    [[maybe_unused]] void* ctx_ = nullptr;
+    void* ctx_ = nullptr;
 };
 
 void swiglu(const float* gu, float* h, int64_t rows, int64_t n_ff, bool interleaved, void* stream);

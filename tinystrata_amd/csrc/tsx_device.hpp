@@ -492,6 +492,29 @@ __device__ __forceinline__ void q8_1_store32(float x, tsx_block_q8_1* y, int i) 
 }
 
 
+// The MoE block's norm of one row held in LDS (s_row[0..n), written by the calling threads, each of which passes the
+// sum of the squares of the values it wrote, in its own order): the sums over each wave, then over the waves in
+// order, give r = 1 / sqrt(sum / n + eps); h[i] = (row[i] * r) * w[i] (two roundings) and, when hq is not null, h's
+// Q8_1 image, 32 consecutive lanes per block (n a multiple of 32).  All NT threads of the block take part.
+template <int NT>
+__device__ __forceinline__ void norm_row_out(const float* s_row, float q, int n, const float* __restrict__ w, float eps,
+                                             float* __restrict__ h, tsx_block_q8_1* __restrict__ hq, float* s_red) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = q;
+    __syncthreads();
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < NT / 64; ++k) sum += s_red[k];
+    const float r = rsqrtf(sum / (float) n + eps);
+    for (int i = threadIdx.x; i < n; i += NT) {
+        const float hv = s_row[i] * r * w[i];
+        h[i] = hv;
+        if (hq) q8_1_store32(hv, hq + i / 32, i & 31);
+    }
+}
+
 // the wave's largest (smallest) 32-bit unsigned value, the same in every lane (all 64 lanes active): four DPP steps
 // within each 16-lane row, two row broadcasts (lane 15 of rows 0 and 2 into rows 1 and 3, then lane 31 into rows 2
 // and 3), and lane 63 read out.  Lanes a step does not write keep `old`, the operation's identity.

@@ -57,6 +57,7 @@ constexpr int kWLoadsA = kSlabA / kWavesA / 16 / 64;  // 16-byte loads per lane 
 constexpr int kXLoads = 2;            // activation quads per thread per round of launch A
 constexpr int kThreadsB = 1024;
 constexpr int kRowsB = 8;             // output rows per block of launch B
+constexpr int kNormRowThreads = 1024;  // the norm launch: threads per token row
 constexpr int kSlabB = 64 * 1024;     // most LDS bytes of a chunk of groups' down rows (8 rows of each)
 constexpr int kBLoads = kSlabB / 16 / kThreadsB;  // 16-byte loads per thread in flight: a whole chunk
 constexpr int kHLoads = 3;            // 16-byte pieces of h per thread prefetched by launch B
@@ -740,6 +741,34 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     }
 }
 
+// the MoE block's end (optional third launch, one block per token): h = (y * r) * norm_w, r = 1 / sqrt(mean(y^2) +
+// eps), and h's Q8_1 image - tsx_moe_combine_norm's norm half.  A separate launch: the norm needs every column of y,
+// which launch B's blocks finish on different XCDs, and a cross-block hand-off inside launch B (device-scope stores,
+// a completion count, device-scope loads) measured slower than the launch boundary
+__global__ void __launch_bounds__(kNormRowThreads) layer_norm_kernel(const float* __restrict__ y, int n,
+                                                                     const float* __restrict__ norm_w, float eps,
+                                                                     float* __restrict__ h, tsx_block_q8_1* __restrict__ hq) {
+    constexpr int kPer = 4096 / kNormRowThreads;  // n <= 4096: every value's load in flight at once
+    __shared__ float s_row[4096];
+    __shared__ float s_red[kNormRowThreads / 64];
+    const int t = blockIdx.x;
+    float v[kPer];
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+        const int i = threadIdx.x + kNormRowThreads * m;
+        v[m] = i < n ? y[(int64_t) t * n + i] : 0.f;
+    }
+    float q = 0.f;
+#pragma unroll
+    for (int m = 0; m < kPer; ++m) {
+        const int i = threadIdx.x + kNormRowThreads * m;
+        if (i < n) s_row[i] = v[m];
+        q += v[m] * v[m];
+    }
+    norm_row_out<kNormRowThreads>(s_row, q, n, norm_w, eps, h + (int64_t) t * n, hq ? hq + (int64_t) t * (n / 32) : nullptr,
+                                  s_red);
+}
+
 template <typename F>
 int with_type(int type, F&& f) {
     switch (type) {
@@ -833,9 +862,11 @@ TSX_API size_t tsx_moe_decode_layer_scratch_bytes(int n_tok, int k, int64_t n_ff
     return kTablesBytes + ((h + 255) & ~(size_t) 255);
 }
 
-TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t stride, int n_expert, int k,
-                                 int n_tok, const float* logits, const float* x, const void* shared, const float* sgate,
-                                 int sg_stride, float* y, int32_t* ids, float* wts, void* scratch, void* stream) {
+// tsx_moe_decode_layer, and with norm_w the norm epilogue of tsx_moe_decode_layer_norm
+static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t stride, int n_expert, int k,
+                        int n_tok, const float* logits, const float* x, const void* shared, const float* sgate,
+                        int sg_stride, float* y, int32_t* ids, float* wts, const float* norm_w, float eps, float* h,
+                        void* hq, void* scratch, void* stream) {
     TSX_REQUIRE(Lp != nullptr, "tsx_moe_decode_layer: null layout");
     const tsx_expert_layout L = *Lp;
     if (!tsx_moe_expert_supported(L.gu_type, L.d_type, L.n_embd, L.n_ff) || L.n_embd > 4096 || L.n_ff > 1024 ||
@@ -875,6 +906,8 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
     TSX_REQUIRE(aligned(blobs, 16) && stride % 16 == 0 && (!shared || aligned(shared, 16)) && aligned(scratch, 256) &&
                     aligned(x, 16) && aligned(y, 4) && aligned(logits, 4),
                 "tsx_moe_decode_layer: blobs, stride, shared and x 16-byte aligned, scratch 256-byte aligned");
+    TSX_REQUIRE(!norm_w || (h && aligned(h, 4) && (!hq || aligned(hq, 2)) && L.n_embd % 32 == 0),
+                "tsx_moe_decode_layer_norm: h (4-byte aligned) with norm_w; hq 2-byte aligned");
     LayerArgs a;
     a.L = L;
     a.blobs = (const uint8_t*) blobs;
@@ -933,12 +966,33 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs,
             return launch_status("tsx_moe_decode_layer/gate-up");
         });
     if (rc != TSX_OK) return rc;
-    return with_type(L.d_type, [&](auto T) {
+    rc = with_type(L.d_type, [&](auto T) {
         auto kern = layer_down_kernel<decltype(T)::value>;
         const size_t lds = (size_t) slab_b + fixed_b;
         kern<<<(unsigned) (L.n_embd / kRowsB), kThreadsB, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/down");
     });
+    if (rc != TSX_OK || norm_w == nullptr) return rc;
+    layer_norm_kernel<<<(unsigned) n_tok, kNormRowThreads, 0, s>>>(y, (int) L.n_embd, norm_w, eps, h,
+                                                                  (tsx_block_q8_1*) hq);
+    return launch_status("tsx_moe_decode_layer_norm/norm");
+}
+
+TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t stride, int n_expert, int k,
+                                 int n_tok, const float* logits, const float* x, const void* shared, const float* sgate,
+                                 int sg_stride, float* y, int32_t* ids, float* wts, void* scratch, void* stream) {
+    return decode_layer(Lp, blobs, stride, n_expert, k, n_tok, logits, x, shared, sgate, sg_stride, y, ids, wts, nullptr,
+                        0.f, nullptr, nullptr, scratch, stream);
+}
+
+TSX_API int tsx_moe_decode_layer_norm(const tsx_expert_layout* Lp, const void* blobs, uint64_t stride, int n_expert,
+                                      int k, int n_tok, const float* logits, const float* x, const void* shared,
+                                      const float* sgate, int sg_stride, float* y, int32_t* ids, float* wts,
+                                      const float* norm_w, float eps, float* h, void* hq, void* scratch,
+                                      void* stream) {
+    TSX_REQUIRE(norm_w != nullptr, "tsx_moe_decode_layer_norm: null norm_w (tsx_moe_decode_layer has no norm)");
+    return decode_layer(Lp, blobs, stride, n_expert, k, n_tok, logits, x, shared, sgate, sg_stride, y, ids, wts, norm_w,
+                        eps, h, hq, scratch, stream);
 }
 
 TSX_API size_t tsx_moe_decode_layer_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }

@@ -286,6 +286,41 @@ __global__ void __launch_bounds__(256) combine4_kernel(float* __restrict__ x, co
     *xo = float4{xv.x + acc.x, xv.y + acc.y, xv.z + acc.z, xv.w + acc.w};
 }
 
+// tsx_moe_combine's arithmetic per value, then the norm (norm_row_out): one block per token row, the combined row
+// kept in LDS
+constexpr int kNormThreads = 256;
+constexpr int kNormMaxK = 16;
+__global__ void __launch_bounds__(kNormThreads) combine_norm_kernel(float* __restrict__ x, const float* __restrict__ parts,
+                                                                   const int32_t* __restrict__ prow,
+                                                                   const float* __restrict__ wts, int k,
+                                                                   const float* __restrict__ shared,
+                                                                   const float* __restrict__ sgate, int sg_stride, int n,
+                                                                   const float* __restrict__ norm_w, float eps,
+                                                                   float* __restrict__ h, tsx_block_q8_1* __restrict__ hq) {
+#pragma clang fp contract(off)
+    extern __shared__ float s_row[];
+    __shared__ const float* s_part[kNormMaxK];
+    __shared__ float s_red[kNormThreads / 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (tid < k) s_part[tid] = parts + (int64_t) (prow ? prow[t * k + tid] : t * k + tid) * n;
+    __syncthreads();
+    const float* wr = wts + (int64_t) t * k;
+    const float gs = shared ? 1.0f / (1.0f + expf(-sgate[(int64_t) t * sg_stride])) : 0.f;
+    float* xr = x + (int64_t) t * n;
+    float q = 0.f;
+    for (int i = tid; i < n; i += kNormThreads) {
+        float acc = wr[0] * s_part[0][i];
+        for (int j = 1; j < k; ++j) acc = __builtin_fmaf(wr[j], s_part[j][i], acc);
+        if (shared) acc += gs * shared[(int64_t) t * n + i];
+        const float v = xr[i] + acc;
+        xr[i] = v;
+        s_row[i] = v;
+        q += v * v;
+    }
+    norm_row_out<kNormThreads>(s_row, q, n, norm_w, eps, h + (int64_t) t * n, hq ? hq + (int64_t) t * (n / 32) : nullptr,
+                               s_red);
+}
+
 }  // namespace
 }  // namespace tsx
 
@@ -370,6 +405,22 @@ TSX_API int tsx_moe_combine(float* x, const float* parts, const int32_t* prow, c
     combine_kernel<<<dim3((unsigned) ((n + 255) / 256), (unsigned) n_tok), 256, 0, (hipStream_t) stream>>>(
         x, parts, prow, wts, k, shared, sgate, sg_stride, n);
     return launch_status("tsx_moe_combine");
+}
+
+TSX_API int tsx_moe_combine_norm(float* x, const float* parts, const int32_t* prow, const float* wts, int k,
+                                 const float* shared, const float* sgate, int sg_stride, int n, int n_tok,
+                                 const float* norm_w, float eps, float* h, void* hq, void* stream) {
+    TSX_REQUIRE(x && parts && wts && norm_w && h && k >= 1 && k <= kNormMaxK && n_tok >= 0 && (!shared || sgate),
+                "tsx_moe_combine_norm: x, parts, wts, norm_w, h, k 1..16 (and sgate with shared)");
+    if (n < 32 || n % 32 != 0 || n > 16384) {
+        set_error("tsx_moe_combine_norm: n = %d (a multiple of 32 up to 16384)", n);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    TSX_REQUIRE(aligned(hq, 2), "tsx_moe_combine_norm: hq 2-byte aligned");
+    if (n_tok == 0) return TSX_OK;
+    combine_norm_kernel<<<(unsigned) n_tok, kNormThreads, (size_t) n * 4, (hipStream_t) stream>>>(
+        x, parts, prow, wts, k, shared, sgate, sg_stride, n, norm_w, eps, h, (tsx_block_q8_1*) hq);
+    return launch_status("tsx_moe_combine_norm");
 }
 
 }  // extern "C"

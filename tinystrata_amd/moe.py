@@ -132,15 +132,28 @@ class MoELayer:
                     self.sgu = torch.empty((n_tok, 2 * self.FF), dtype=f32, device=dev)
                     self.sh_h = torch.empty((n_tok, self.FF), dtype=f32, device=dev)
 
-    def __call__(self, x: torch.Tensor, logits: torch.Tensor, sgate: torch.Tensor | None, y: torch.Tensor) -> None:
-        """y += MoE(x): x, y [n_tok, N] float32; logits [n_tok, E]; sgate [n_tok] (shared expert gate logit)."""
+    def __call__(self, x: torch.Tensor, logits: torch.Tensor, sgate: torch.Tensor | None, y: torch.Tensor,
+                 norm_w: torch.Tensor | None = None, eps: float = 1e-6, h: torch.Tensor | None = None,
+                 hq: torch.Tensor | None = None) -> None:
+        """y += MoE(x): x, y [n_tok, N] float32; logits [n_tok, E]; sgate [n_tok] (shared expert gate logit).  With
+        norm_w [N], the MoE block's end as well: h [n_tok, N] = rms(y) * norm_w and, hq given, its Q8_1 image."""
+        self._norm = (norm_w, eps, h, hq)
         (self._decode if self.decode else self._prefill)(x, logits, sgate, y)
+
+    def _combine(self, y, sgate, prow=None):
+        norm_w, eps, h, hq = self._norm
+        if norm_w is None:
+            ops.moe_combine(y, self.parts, self.wts, self.k, prow=prow, shared=self.sh, sgate=sgate)
+        else:
+            ops.moe_combine_norm(y, self.parts, self.wts, self.k, norm_w, eps, h, hq, prow=prow, shared=self.sh,
+                                 sgate=sgate)
 
     def _decode(self, x, logits, sgate, y):
         W, L, k = self.W, self.W.L, self.k
         if self.fused:
+            norm_w, eps, h, hq = self._norm
             ops.moe_decode_layer(L, W.blobs, W.stride, W.n_expert, k, logits, x, y, self.ids, self.wts, self.lscratch,
-                                 shared=W.shared, sgate=sgate)
+                                 shared=W.shared, sgate=sgate, norm_w=norm_w, eps=eps, h=h, hq=hq)
             return
         ops.native_router_topk(logits, k, self.ids, self.wts)
         gp, gs, ng, ed, et = ops.group_entries(self.ids, k, W.n_expert, W.base, W.stride, bufs=self.grp)
@@ -152,7 +165,7 @@ class MoELayer:
             ops.iq_mmvq(L.gu_type, sh[L.up_off:], self.xq, self.N, self.FF, self.n_tok, y=self.su)
             ops.native_swiglu_quantize_q8_1(self.sg, self.su, self.shq)
             ops.iq_mmvq(L.d_type, sh[L.down_off:], self.shq, self.FF, self.N, self.n_tok, y=self.sh)
-        ops.moe_combine(y, self.parts, self.wts, k, shared=self.sh, sgate=sgate)
+        self._combine(y, sgate)
 
     def _prefill(self, x, logits, sgate, y):
         W, L, k, N, FF = self.W, self.W.L, self.k, self.N, self.FF
@@ -176,7 +189,7 @@ class MoELayer:
             ops.mmq_swiglu(self.sgu, T, FF, False, h=self.sh_h)
             ops.mmq_quantize(self.sh_h, None, L.d_type, FF, FF, T, xq=self.shq)
             ops.mmq_run(sh[L.down_off:], L.d_type, N, FF, W.stride, 1, self.shq, self.sh_bounds, None, T, self.sh, N)
-        ops.moe_combine(y, self.parts, self.wts, k, prow=rinv, shared=self.sh, sgate=sgate)
+        self._combine(y, sgate, prow=rinv)
 
     def _prefill_fused(self, x, sgate, y, bounds, et, rinv):
         W, L, k, N, FF, T = self.W, self.W.L, self.k, self.N, self.FF, self.n_tok
@@ -189,4 +202,4 @@ class MoELayer:
             sh = W.shared
             ops.mmq_gate_up_swiglu(sh, L.gu_type, FF, N, W.stride, 1, self.txq, T, None, self.sh_bounds, T, hq=self.shq)
             ops.mmq_run(sh[L.down_off:], L.d_type, N, FF, W.stride, 1, self.shq, self.sh_bounds, None, T, self.sh, N)
-        ops.moe_combine(y, self.parts, self.wts, k, prow=rinv, shared=self.sh, sgate=sgate)
+        self._combine(y, sgate, prow=rinv)

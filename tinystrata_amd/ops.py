@@ -121,12 +121,19 @@ def decode_layer_scratch_bytes(n_tok: int, k: int, n_ff: int) -> int:
 
 
 def moe_decode_layer(L: ExpertLayout, blobs, stride: int, n_expert: int, k: int, logits, x, y, ids, wts, scratch,
-                     shared=None, sgate=None, sg_stride: int = 1, stream=None) -> None:
-    """y += the whole decode MoE layer of x (1..8 tokens) in two launches (tsx_moe_decode_layer)."""
+                     shared=None, sgate=None, sg_stride: int = 1, stream=None, norm_w=None, eps: float = 1e-6,
+                     h=None, hq=None) -> None:
+    """y += the whole decode MoE layer of x (1..8 tokens) in two launches (tsx_moe_decode_layer); with norm_w, also
+    h = rms(y) * norm_w and (hq given) its Q8_1 image (tsx_moe_decode_layer_norm)."""
     n_tok = x.shape[0]
-    check(lib().tsx_moe_decode_layer(C.byref(L), _p(blobs), stride, n_expert, k, n_tok, _p(logits), _p(x), _p(shared),
-                                     _p(sgate), sg_stride, _p(y), _p(ids), _p(wts), _p(scratch), _stream(stream)),
-          "moe_decode_layer")
+    if norm_w is None:
+        check(lib().tsx_moe_decode_layer(C.byref(L), _p(blobs), stride, n_expert, k, n_tok, _p(logits), _p(x),
+                                         _p(shared), _p(sgate), sg_stride, _p(y), _p(ids), _p(wts), _p(scratch),
+                                         _stream(stream)), "moe_decode_layer")
+        return
+    check(lib().tsx_moe_decode_layer_norm(C.byref(L), _p(blobs), stride, n_expert, k, n_tok, _p(logits), _p(x),
+                                          _p(shared), _p(sgate), sg_stride, _p(y), _p(ids), _p(wts), _p(norm_w), eps,
+                                          _p(h), _p(hq), _p(scratch), _stream(stream)), "moe_decode_layer_norm")
 
 
 # ------------------------------------------------------------------ routing
@@ -190,6 +197,14 @@ def moe_combine(x, parts, wts, k: int, prow=None, shared=None, sgate=None, sg_st
     n_tok, n = x.shape
     check(lib().tsx_moe_combine(_p(x), _p(parts), _p(prow), _p(wts), k, _p(shared), _p(sgate), sg_stride, n, n_tok,
                                 _stream(stream)), "moe_combine")
+
+
+def moe_combine_norm(x, parts, wts, k: int, norm_w, eps: float, h, hq=None, prow=None, shared=None, sgate=None,
+                     sg_stride: int = 1, stream=None) -> None:
+    """moe_combine, then h = rms(x) * norm_w and (hq given) its Q8_1 image: the MoE block's end (k_moe_out)."""
+    n_tok, n = x.shape
+    check(lib().tsx_moe_combine_norm(_p(x), _p(parts), _p(prow), _p(wts), k, _p(shared), _p(sgate), sg_stride, n, n_tok,
+                                     _p(norm_w), eps, _p(h), _p(hq), _stream(stream)), "moe_combine_norm")
 
 
 # ------------------------------------------------------------------ prefill
