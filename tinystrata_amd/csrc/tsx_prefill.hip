@@ -188,7 +188,10 @@ __global__ void __launch_bounds__(kThreads) mmq_rows_kernel(const uint8_t* __res
 // (0x64XX - 1152 = XX - 128 per byte).  K advances one 256-value chunk at a time; the next chunk's weight pieces and
 // activation codes are in flight in registers while the current one is multiplied, and the activation tile is
 // double-buffered when LDS allows (one block barrier per chunk).
-constexpr int kBN = 64;
+// sorted token rows per block tile: 128 for the codebook formats (the decode of a weight fragment serves more tokens,
+// and an expert's weights are read once per 128 of its rows); 64 for Q4_K (its experts are mostly small, and at 64
+// the activation tile is double-buffered: one barrier per chunk) and Q8_0 (its wider raw rows fill the LDS)
+template <int T> constexpr int bn_of() { return T == TSX_Q8_0 || T == TSX_Q4_K ? 64 : 128; }
 constexpr int kChunk = 256;
 constexpr int kBStride = kChunk + 8;  // fp16 per activation-tile row: 528 bytes puts 16 lanes' 16-byte reads on all banks
 constexpr int kMaxExpertsMmq = 512;
@@ -240,11 +243,37 @@ template <int T> constexpr bool chunk_aligned() { return chunk_bytes<T>() % 16 =
 template <int T> constexpr int raw_stride() {
     return ((chunk_bytes<T>() + (chunk_aligned<T>() ? 0 : 15) + 15) / 16 | 1) * 16;
 }
-template <int T, int NW, int NB> constexpr int f16_lds_bytes() {
-    return NB * (kBN * kBStride * 2 + kBN * 8 * 4 * (T == TSX_Q4_K ? 2 : 1)) + NW * 32 * raw_stride<T>() +
-           half_table_words<T>() * 4 + NW * (32 * 4 + 8 * 32 * 4 * 3) + 64;
+// silu(g) * u as the prompt path forms it (the fused gate/up epilogue and mmq_swiglu_kernel alike): g / (1 + e^-g)
+// with e^-g = 2^(-g log2 e) on the hardware exp2 and the quotient as g times the hardware reciprocal, the product
+// rounded on its own.  Within a few ulps of g / (1 + expf(-g)) * u: the prompt layer's parity is 1e-3 relative L2,
+// and this is the epilogue's dominant cost with the library exp and an IEEE division (~5 vs ~25 instructions)
+__device__ __forceinline__ float prompt_swiglu(float g, float u) {
+#pragma clang fp contract(off)
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504f);
+    return (g * __builtin_amdgcn_rcpf(1.0f + e)) * u;
 }
-template <int T, int NW> constexpr int f16_buffers() { return f16_lds_bytes<T, NW, 2>() <= 150 * 1024 ? 2 : 1; }
+
+// the hand-laid LDS of mmq_f16_kernel: the codebooks at address 0 and the arrays read per unit next, so that their
+// addresses fit the 16-bit offsets of the LDS instructions; the raw weight slabs and the activation tiles last (the
+// compiler would order separate arrays by size, the large ones first)
+template <int T, int NW, int NB> struct F16Layout {
+    static constexpr bool Q4K = T == TSX_Q4_K, Q80 = T == TSX_Q8_0, XXS = T == TSX_IQ3_XXS;
+    static constexpr int TW = half_table_words<T>();
+    static constexpr int TAB = 0, AM = TAB + lds_round((TW > 0 ? TW : 4) * 4);
+    static constexpr int SC = AM + lds_round((XXS ? NW : 1) * 8 * 32 * 8);
+    static constexpr int UF = SC + lds_round((XXS ? 1 : NW) * 8 * 32 * 4);
+    static constexpr int RW = UF + lds_round((Q4K || Q80 ? NW : 1) * 8 * 32 * 4);
+    static constexpr int DW = RW + lds_round(NW * 32 * 4);
+    static constexpr int RHO = DW + lds_round(NW * 32 * 4);
+    static constexpr int BN = bn_of<T>();
+    static constexpr int DL = RHO + lds_round(NB * BN * 8 * 4);
+    static constexpr int DM = DL + lds_round(BN * 4);
+    static constexpr int SCAN = DM + lds_round((Q4K ? NB * BN : 1) * 8 * 4);
+    static constexpr int RAW = SCAN + lds_round((NW + 2) * 4);
+    static constexpr int TB = RAW + lds_round(NW * 32 * raw_stride<T>());
+    static constexpr int BYTES = TB + NB * BN * kBStride * 2;
+};
+template <int T, int NW> constexpr int f16_buffers() { return F16Layout<T, NW, 2>::BYTES <= 150 * 1024 ? 2 : 1; }
 
 __device__ __forceinline__ uint32_t hmul(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
@@ -310,38 +339,29 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                                                           const int32_t* __restrict__ ids, float* __restrict__ dst,
                                                           int64_t ld_dst, const int32_t* __restrict__ xids = nullptr,
                                                           MmqPlanes H = MmqPlanes{}, int n_ff = 0) {
-    constexpr int NT = 64 * NW, BM = 32 * NW, NB = f16_buffers<T, NW>();
+    constexpr int NT = 64 * NW, BM = 32 * NW, NB = f16_buffers<T, NW>(), kBN = bn_of<T>();
     constexpr int CB = chunk_bytes<T>(), RS = raw_stride<T>(), PR = RS / 16, RW = (32 * PR + 63) / 64;
-    constexpr int BP = kBN * 16 / NT, DP = kBN * 8 / NT, EPT = kMaxExpertsMmq / NT;
+    constexpr int BP = kBN * 16 / NT, EPT = kMaxExpertsMmq / NT;
     constexpr int TW = half_table_words<T>(), GW = half_grid_words<T>(), TPT = (TW + NT - 1) / NT;
     constexpr bool Q4K = T == TSX_Q4_K, Q80 = T == TSX_Q8_0, IQ3S = T == TSX_IQ3_S;
-    // LDS as one array laid out by hand: the codebooks at address 0 and the arrays read per unit next, so that
-    // their addresses fit the 16-bit offsets of the LDS instructions; the raw weight slabs and the activation tiles
-    // last (the compiler would order separate arrays by size, the large ones first)
     constexpr int XXS = T == TSX_IQ3_XXS;
-    constexpr int O_TAB = 0, O_AM = O_TAB + lds_round((TW > 0 ? TW : 4) * 4);
-    constexpr int O_SC = O_AM + lds_round((XXS ? NW : 1) * 8 * 32 * 8);
-    constexpr int O_UF = O_SC + lds_round((IQ3S || Q4K ? NW : 1) * 8 * 32 * 4);
-    constexpr int O_RD = O_UF + lds_round((Q4K || Q80 ? NW : 1) * 8 * 32 * 4);
-    constexpr int O_DX = O_RD + lds_round(NW * 32 * 4);
-    constexpr int O_DM = O_DX + lds_round(NB * kBN * 8 * 4);
-    constexpr int O_SCAN = O_DM + lds_round((Q4K ? NB * kBN : 1) * 8 * 4);
-    constexpr int O_RAW = O_SCAN + lds_round((NW + 2) * 4);
-    constexpr int O_TB = O_RAW + lds_round(NW * 32 * RS);
-    constexpr int LDS_BYTES = O_TB + NB * kBN * kBStride * 2;
-    __shared__ __attribute__((aligned(16))) uint8_t s_lds[LDS_BYTES];
-    auto& s_tab = *reinterpret_cast<uint32_t(*)[TW > 0 ? TW : 4]>(s_lds + O_TAB);
-    auto& s_am = *reinterpret_cast<uint2(*)[XXS ? NW : 1][8][32]>(s_lds + O_AM);         // IQ3_XXS: aux word, m pair
-    auto& s_sc = *reinterpret_cast<uint32_t(*)[IQ3S || Q4K ? NW : 1][8][32]>(s_lds + O_SC);  // integer scale, fp16 pair
-    auto& s_uf = *reinterpret_cast<float(*)[Q4K || Q80 ? NW : 1][8][32]>(s_lds + O_UF);     // Q4_K: dmin * m; Q8_0: d
-    auto& s_rd = *reinterpret_cast<float(*)[NW][32]>(s_lds + O_RD);                         // row scale per chunk
-    auto& s_dx = *reinterpret_cast<float(*)[NB][kBN][8]>(s_lds + O_DX);
-    auto& s_dm = *reinterpret_cast<float(*)[Q4K ? NB : 1][Q4K ? kBN : 1][8]>(s_lds + O_DM);
-    int* const s_scan = reinterpret_cast<int*>(s_lds + O_SCAN);
+    static_assert(kBN <= NT, "one thread per token stages the token's scales");
+    using L = F16Layout<T, NW, NB>;
+    __shared__ __attribute__((aligned(16))) uint8_t s_lds[L::BYTES];
+    auto& s_tab = *reinterpret_cast<uint32_t(*)[TW > 0 ? TW : 4]>(s_lds + L::TAB);
+    auto& s_am = *reinterpret_cast<uint2(*)[XXS ? NW : 1][8][32]>(s_lds + L::AM);  // IQ3_XXS: aux word, scale pair
+    auto& s_sc = *reinterpret_cast<uint32_t(*)[XXS ? 1 : NW][8][32]>(s_lds + L::SC);  // scale pair (Q8_0: 0/1 mask)
+    auto& s_uf = *reinterpret_cast<float(*)[Q4K || Q80 ? NW : 1][8][32]>(s_lds + L::UF);  // Q4_K: dmin m / w'; Q8_0: ratio
+    auto& s_rw = *reinterpret_cast<float(*)[NW][32]>(s_lds + L::RW);  // row ratio at the chunk's first unit
+    auto& s_dw = *reinterpret_cast<float(*)[NW][32]>(s_lds + L::DW);  // the row's scale w' so far
+    auto& s_rho = *reinterpret_cast<float(*)[NB][kBN][8]>(s_lds + L::RHO);  // token ratio per unit
+    float* const s_dl = reinterpret_cast<float*>(s_lds + L::DL);             // the token's D' so far
+    auto& s_dm = *reinterpret_cast<float(*)[Q4K ? NB : 1][Q4K ? kBN : 1][8]>(s_lds + L::DM);
+    int* const s_scan = reinterpret_cast<int*>(s_lds + L::SCAN);
     int& s_x = s_scan[NW];
     int& s_tile0 = s_scan[NW + 1];
-    auto& s_raw = *reinterpret_cast<uint8_t(*)[NW][32 * RS]>(s_lds + O_RAW);
-    auto& tB = *reinterpret_cast<_Float16(*)[NB][kBN * kBStride]>(s_lds + O_TB);
+    auto& s_raw = *reinterpret_cast<uint8_t(*)[NW][32 * RS]>(s_lds + L::RAW);
+    auto& tB = *reinterpret_cast<_Float16(*)[NB][kBN * kBStride]>(s_lds + L::TB);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int bx = blockIdx.x, by = blockIdx.y;
@@ -376,22 +396,24 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) wrow * row_bytes;
     const int nu = w_cols / 32, nchunks = w_cols / kChunk;
     // the activation rows this thread loads (the same every chunk): rows past the tile's last take its last row
-    int64_t arow_b[BP], arow_d[DP];
+    int64_t arow_b[BP];
 #pragma unroll
     for (int h = 0; h < BP; ++h) {
-        const int rr = (tid + NT * h) >> 4;
-        arow_b[h] = xids ? (int64_t) xids[row0 + min(rr, nrows - 1)] : (int64_t) (row0 + rr);
+        const int r = row0 + min((tid + NT * h) >> 4, nrows - 1);
+        arow_b[h] = xids ? (int64_t) xids[r] : (int64_t) r;
     }
-#pragma unroll
-    for (int h = 0; h < DP; ++h) {
-        const int rr = (tid + NT * h) >> 3;
-        arow_d[h] = xids ? (int64_t) xids[row0 + min(rr, nrows - 1)] : (int64_t) (row0 + rr);
+    // thread tid < kBN stages token tid's scales (tokens past the tile's last take its last row's)
+    int64_t arow_s;
+    {
+        const int r = row0 + min(tid, nrows - 1);
+        arow_s = xids ? (int64_t) xids[r] : (int64_t) r;
     }
 
-    // chunk c in flight: this wave's raw weight pieces, the block's share of activation codes and scales
+    // chunk c in flight: this wave's raw weight pieces, the block's share of activation codes, and (threads below
+    // kBN) a token's eight block scales (Q4_K: and code sums)
     v4i rw[RW], av[BP];
-    float ad[DP];
-    int am[DP];
+    float4 ad[2];
+    int4 am4[2];
     auto fetch = [&](int c) {
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
@@ -405,14 +427,24 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             const int pi = tid + NT * h, q = pi & 15;
             av[h] = *(const v4i*) (P.q + arow_b[h] * P.cols + kChunk * c + 16 * q);
         }
-#pragma unroll
-        for (int h = 0; h < DP; ++h) {
-            const int e = tid + NT * h, u = e & 7;
-            const int64_t o = arow_d[h] * nu + 8 * c + u;
-            ad[h] = P.d[o];
-            if constexpr (Q4K) am[h] = P.m[o];
+        if (tid < kBN) {
+            const float4* dp = (const float4*) (P.d + arow_s * nu + 8 * c);
+            ad[0] = dp[0];
+            ad[1] = dp[1];
+            if constexpr (Q4K) {
+                const int4* mp = (const int4*) (P.m + arow_s * nu + 8 * c);
+                am4[0] = mp[0];
+                am4[1] = mp[1];
+            }
         }
     };
+    // The outputs are accumulated in the scale of the current unit: before unit u's products are added, the
+    // accumulator is multiplied by D'(u-1) / D'(u) for its token and, at a chunk's first unit, w'(c-1) / w'(c) for
+    // its row (D' the token's Q8_1 scale of the unit, w' the row's float scale of the chunk; a zero scale takes the
+    // last nonzero one, its codes or weights contributing zero), and the result is multiplied by the last D' and w'
+    // at the end.  Scales are fp16 values, so every ratio lies in [2^-40, 2^40] and the accumulator stays far from
+    // overflow.  Here: the token's ratios for the chunk's eight units, D' after them, and (Q4_K) the min term's
+    // activation factor dx * (code sum) / D'(the chunk's last unit).
     auto stage = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < RW; ++i)
@@ -427,11 +459,31 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             d[0] = v4i{(int) o[0], (int) o[1], (int) o[2], (int) o[3]};
             d[1] = v4i{(int) o[4], (int) o[5], (int) o[6], (int) o[7]};
         }
+        if (tid < kBN) {
+            const float d8[8] = {ad[0].x, ad[0].y, ad[0].z, ad[0].w, ad[1].x, ad[1].y, ad[1].z, ad[1].w};
+            float prev = s_dl[tid], rho[8], dn8[8];
 #pragma unroll
-        for (int h = 0; h < DP; ++h) {
-            const int e = tid + NT * h, rr = e >> 3, u = e & 7;
-            s_dx[buf][rr][u] = ad[h];
-            if constexpr (Q4K) s_dm[buf][rr][u] = ad[h] * (float) am[h];
+            for (int u = 0; u < 8; ++u) {
+                const float dn = d8[u] != 0.f ? d8[u] : prev;
+                rho[u] = prev / dn;
+                dn8[u] = dn;
+                prev = dn;
+            }
+            s_dl[tid] = prev;
+            float4* rp = (float4*) s_rho[buf][tid];
+            rp[0] = float4{rho[0], rho[1], rho[2], rho[3]};
+            rp[1] = float4{rho[4], rho[5], rho[6], rho[7]};
+            if constexpr (Q4K) {
+                const int m8[8] = {am4[0].x, am4[0].y, am4[0].z, am4[0].w, am4[1].x, am4[1].y, am4[1].z, am4[1].w};
+                float mf[8];
+                const float rp = 1.0f / prev;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) mf[u] = d8[u] * (float) m8[u] * rp;
+                float4* mq = (float4*) s_dm[buf][tid];
+                mq[0] = float4{mf[0], mf[1], mf[2], mf[3]};
+                mq[1] = float4{mf[4], mf[5], mf[6], mf[7]};
+            }
+            (void) dn8;
         }
     };
 
@@ -445,6 +497,8 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             tw[k] = i < GW ? src[i] : sgn[i - GW];
         }
     }
+    if (tid < kBN) s_dl[tid] = 1.0f;   // read back only by the same thread (stage)
+    if (lane < 32) s_dw[wave][lane] = 1.0f;  // read back only by the same wave (the row factors)
     fetch(0);
     if constexpr (TW > 0) {
 #pragma unroll
@@ -458,61 +512,77 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     // the chunk loop, specialised on the number of 16-token tiles that hold rows (no per-tile branches inside)
     auto run = [&](auto ntt_c) {
         constexpr int NTT = decltype(ntt_c)::value;
-        float acc[2][NTT][4], tacc[2][NTT][4];
+        float acc[2][NTT][4];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int tj = 0; tj < NTT; ++tj)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][tj][i] = tacc[t][tj][i] = 0.f;
+                for (int i = 0; i < 4; ++i) acc[t][tj][i] = 0.f;
 
         for (int c = 0; c < nchunks; ++c) {
             const int buf = NB == 2 ? (c & 1) : 0;
             const _Float16* B = tB[buf];
             const uint8_t* slab = s_raw[wave];
             const lds_ptr<const v4i> bq = lds_base<v4i>(B + lr * kBStride + 8 * g);  // this lane's activation pieces
-            // the wave's rows: per-row and per-unit factors (lane = row r, units 4 hl .. 4 hl + 3)
+            // the wave's rows: the chunk's row scale w' and ratio, and the per-unit integer scales (lane = row r,
+            // units 4 hl .. 4 hl + 3); a zero row scale zeroes the row's weights for the chunk
             {
                 const int r = lane & 31, hl = lane >> 5;
                 const uint8_t* b = slab + r * RS + (int) (((uint64_t) r * row_bytes + (uint64_t) c * CB) & 15);
-                if constexpr (T == TSX_IQ3_XXS) {
-                    if (hl == 0) s_rd[wave][r] = 0.25f * h2f((uint16_t) ld16(b));
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int j = 4 * hl + k;
-                        const uint32_t aux = ld32a2(b + 66 + 4 * j);
-                        s_am[wave][j][r] = uint2{aux, hpair(2 * (aux >> 28) + 1)};
+                const float wold = s_dw[wave][r];
+                if constexpr (T == TSX_IQ3_XXS || IQ3S || Q4K) {
+                    const float d = h2f((uint16_t) ld16(b));
+                    const float dw = XXS ? 0.25f * d : d;
+                    const float wn = dw != 0.f ? dw : wold;
+                    const bool live = dw != 0.f;
+                    if (hl == 0) {
+                        s_rw[wave][r] = wold / wn;
+                        s_dw[wave][r] = wn;
                     }
-                } else if constexpr (IQ3S) {
-                    if (hl == 0) s_rd[wave][r] = h2f((uint16_t) ld16(b));
+                    if constexpr (T == TSX_IQ3_XXS) {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int j = 4 * hl + k;
-                        s_sc[wave][j][r] = hpair(2 * ((b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u) + 1);
-                    }
-                } else if constexpr (Q4K) {
-                    const float d = h2f((uint16_t) ld16(b)), dmin = h2f((uint16_t) ld16(b + 2));
-                    if (hl == 0) s_rd[wave][r] = d;
-                    const uint8_t* s12 = b + 4;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int j = 4 * hl + k;
-                        int sc, m;
-                        if (j < 4) {
-                            sc = s12[j] & 63;
-                            m = s12[j + 4] & 63;
-                        } else {
-                            sc = (s12[j + 4] & 15) | ((s12[j - 4] >> 6) << 4);
-                            m = (s12[j + 4] >> 4) | ((s12[j] >> 6) << 4);
+                        for (int k = 0; k < 4; ++k) {
+                            const int j = 4 * hl + k;
+                            const uint32_t aux = ld32a2(b + 66 + 4 * j);
+                            s_am[wave][j][r] = uint2{aux, live ? hpair(2 * (aux >> 28) + 1) : 0u};
                         }
-                        s_sc[wave][j][r] = hpair((uint32_t) sc);
-                        s_uf[wave][j][r] = dmin * (float) m;
-                    }
-                } else {
+                    } else if constexpr (IQ3S) {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int j = 4 * hl + k;
-                        s_uf[wave][j][r] = h2f((uint16_t) ld16(b + 34 * j));
+                        for (int k = 0; k < 4; ++k) {
+                            const int j = 4 * hl + k;
+                            s_sc[wave][j][r] = live ? hpair(2 * ((b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u) + 1) : 0u;
+                        }
+                    } else {
+                        const float dmin = h2f((uint16_t) ld16(b + 2)), dr = dmin / wn;
+                        const uint8_t* s12 = b + 4;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const int j = 4 * hl + k;
+                            int sc, m;
+                            if (j < 4) {
+                                sc = s12[j] & 63;
+                                m = s12[j + 4] & 63;
+                            } else {
+                                sc = (s12[j + 4] & 15) | ((s12[j - 4] >> 6) << 4);
+                                m = (s12[j + 4] >> 4) | ((s12[j] >> 6) << 4);
+                            }
+                            s_sc[wave][j][r] = live ? hpair((uint32_t) sc) : 0u;
+                            s_uf[wave][j][r] = dr * (float) m;
+                        }
+                    }
+                } else {  // Q8_0: a float scale per unit, its ratio applied at every unit
+                    if (hl == 0) {
+                        float wv = wold;
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const float d = h2f((uint16_t) ld16(b + 34 * j));
+                            const float wn = d != 0.f ? d : wv;
+                            s_uf[wave][j][r] = wv / wn;
+                            s_sc[wave][j][r] = d != 0.f ? 0x3C003C00u : 0u;
+                            wv = wn;
+                        }
+                        s_dw[wave][r] = wv;
                     }
                 }
             }
@@ -564,68 +634,61 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                         nib_to_h(w1, sc, nsc, f[2], f[3]);
                     } else {
                         const uint8_t* q = b + 34 * u + 2 + 8 * g;
+                        const uint32_t m = s_sc[wave][u][r];
                         i8_to_h(ld32a2(q), f[0], f[1]);
                         i8_to_h(ld32a2(q + 4), f[2], f[3]);
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) f[k] = hmul(f[k], m);
                     }
                     A[t] = v4i{(int) f[0], (int) f[1], (int) f[2], (int) f[3]};
                 }
             };
-            // unit u's activation fragments and scales (tokens 16 tj + lr)
-            auto load_b = [&](int u, v4i (&Bf)[NTT], float (&dx)[NTT]) {
-#pragma unroll
-                for (int tj = 0; tj < NTT; ++tj) {
-                    const int tok = 16 * tj + lr;
-                    Bf[tj] = bq[(tj * 16 * kBStride + 32 * u) / 8];
-                    dx[tj] = s_dx[buf][tok][u];
-                }
-            };
-            // software pipeline over the chunk's 8 units: unit u + 1's fragments are read and decoded while unit u's
-            // products run on the matrix cores, and each product is scaled only after the next unit's decode
-            v4i A[2], Bf[NTT];
-            float dx[NTT];
-            decode(0, A);
-            load_b(0, Bf, dx);
-#pragma unroll 1
-            for (int u = 0; u < 8; ++u) {
-                v4f D[2][NTT];
-#pragma unroll
-                for (int tj = 0; tj < NTT; ++tj)
-#pragma unroll
-                    for (int t = 0; t < 2; ++t)
-                        D[t][tj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, A[t]),
-                                                                         __builtin_bit_cast(v8h, Bf[tj]),
-                                                                         v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                float dxu[NTT];
-#pragma unroll
-                for (int tj = 0; tj < NTT; ++tj) dxu[tj] = dx[tj];
-                // per-output-row unit factors (Q8_0 scale): rows 16 t + 4 g + i
-                float4 uf[2];
-                if constexpr (Q80) {
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) uf[t] = *(const float4*) &s_uf[wave][u][16 * t + 4 * g];
-                }
-                if (u + 1 < 8) {
-                    decode(u + 1, A);
-                    load_b(u + 1, Bf, dx);
-                }
-#pragma unroll
-                for (int tj = 0; tj < NTT; ++tj)
+            // unit u: every accumulator to the unit's scale (ROW: with the rows' ratios, rows 16 t + 4 g + i), then
+            // the unit's products added in place, token tile by token tile (each tile's activation fragment and
+            // ratio read just before its products); the next unit's weights are decoded while they run
+            v4i A[2];
+            auto step = [&](int u, auto row_c) {
+                constexpr bool ROW = decltype(row_c)::value;
+                float rr[2][4];
+                if constexpr (ROW) {
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
-                        const float ufa[4] = {uf[t].x, uf[t].y, uf[t].z, uf[t].w};
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            if constexpr (Q80) acc[t][tj][i] += (ufa[i] * dxu[tj]) * D[t][tj][i];
-                            else tacc[t][tj][i] += dxu[tj] * D[t][tj][i];
-                        }
+                        const float4 v = Q80 ? *(const float4*) &s_uf[wave][u][16 * t + 4 * g]
+                                             : *(const float4*) &s_rw[wave][16 * t + 4 * g];
+                        rr[t][0] = v.x;
+                        rr[t][1] = v.y;
+                        rr[t][2] = v.z;
+                        rr[t][3] = v.w;
                     }
+                }
 #pragma unroll
-                for (int tj = 0; tj < NTT; ++tj) asm volatile("" ::"v"(Bf[tj]), "v"(dx[tj]));  // read in this step
+                for (int tj = 0; tj < NTT; ++tj) {
+                    const v4i bf = bq[(tj * 16 * kBStride + 32 * u) / 8];
+                    const float rh = s_rho[buf][16 * tj + lr][u];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        v4f C;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) C[i] = acc[t][tj][i] * (ROW ? rh * rr[t][i] : rh);
+                        const v4f D = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, A[t]),
+                                                                            __builtin_bit_cast(v8h, bf), C, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[t][tj][i] = D[i];
+                    }
+                }
+                if (u + 1 < 8) decode(u + 1, A);
+            };
+            decode(0, A);
+            step(0, std::integral_constant<bool, true>{});
+#pragma unroll 1
+            for (int u = 1; u < 8; ++u) {
+                if constexpr (Q80) step(u, std::integral_constant<bool, true>{});
+                else step(u, std::integral_constant<bool, false>{});
             }
             if constexpr (Q4K) {
-                // the chunk's min term, sum over units u of (dmin m)[row][u] * (dx s)[token][u]: a [rows x 8] by
-                // [8 x tokens] product on the fp32 matrix cores (two K = 4 steps), rows 16 t + lr by units 4 h + g
-                // in A, units by tokens 16 tj + lr in B, accumulated into the outputs
+                // the chunk's min term in the chunk's last scale: sum over units u of -(dmin m / w')[row][u] *
+                // (dx s / D'_7)[token][u], a [rows x 8] by [8 x tokens] product on the fp32 matrix cores (two K = 4
+                // steps), rows 16 t + lr by units 4 h + g in A, units by tokens 16 tj + lr in B
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     float am[2];
@@ -644,26 +707,24 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     }
                 }
             }
-            if constexpr (!Q80) {  // the chunk's row scale
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const float4 rd4 = *(const float4*) &s_rd[wave][16 * t + 4 * g];
-                    const float rd[4] = {rd4.x, rd4.y, rd4.z, rd4.w};
-#pragma unroll
-                    for (int tj = 0; tj < NTT; ++tj)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            acc[t][tj][i] += rd[i] * tacc[t][tj][i];
-                            tacc[t][tj][i] = 0.f;
-                        }
-                }
-            }
             if (c + 1 < nchunks) {
                 if constexpr (NB == 1) __syncthreads();  // every wave is done with the single activation tile
                 wave_lds_order();                        // this wave is done with its raw slab and factor rows
                 stage(NB == 2 ? (c + 1) & 1 : 0);
                 if (c + 2 < nchunks) fetch(c + 2);
                 __syncthreads();
+            }
+        }
+        // to the outputs' scale: the row's last w' and the token's last D'
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const float4 w4 = *(const float4*) &s_dw[wave][16 * t + 4 * g];
+            const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int tj = 0; tj < NTT; ++tj) {
+                const float dl = s_dl[16 * tj + lr];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][tj][i] = acc[t][tj][i] * wv[i] * dl;
             }
         }
 
@@ -694,10 +755,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     const float* gp = so + tok * OS + 4 * f4;
                     float hv[4];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const float gt = gp[k];
-                        hv[k] = (gt / (1.0f + expf(-gt))) * gp[BM / 2 + k];
-                    }
+                    for (int k = 0; k < 4; ++k) hv[k] = prompt_swiglu(gp[k], gp[BM / 2 + k]);
                     float amax = fmaxf(fmaxf(fabsf(hv[0]), fabsf(hv[1])), fmaxf(fabsf(hv[2]), fabsf(hv[3])));
                     amax = lanes_reduce<8>(amax, OpMax());
                     const float d = q8_1_finite(amax / 127.0f), rd = 1.0f / d;
@@ -735,10 +793,13 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             }
         }
     };
+    // partial tiles run the next size up in {1, 2, 3, 4, 6, 8} 16-token tiles (the extra ones multiply padding)
     if (ntt == 1) run(std::integral_constant<int, 1>{});
     else if (ntt == 2) run(std::integral_constant<int, 2>{});
     else if (ntt == 3) run(std::integral_constant<int, 3>{});
-    else run(std::integral_constant<int, 4>{});
+    else if (kBN == 64 || ntt == 4) run(std::integral_constant<int, 4>{});
+    else if (kBN == 96 || ntt <= 6) run(std::integral_constant<int, (kBN >= 96 ? 6 : 4)>{});
+    else run(std::integral_constant<int, (kBN >= 128 ? 8 : 4)>{});
 }
 
 __global__ void __launch_bounds__(kThreads) mmq_swiglu_kernel(const float* __restrict__ gu, float* __restrict__ h,
@@ -749,7 +810,7 @@ __global__ void __launch_bounds__(kThreads) mmq_swiglu_kernel(const float* __res
     const int64_t r = i / n_ff, k = i % n_ff;
     const float* row = gu + r * 2 * n_ff;
     const float g = interleaved ? row[2 * k] : row[k], u = interleaved ? row[2 * k + 1] : row[n_ff + k];
-    h[i] = (g / (1.0f + expf(-g))) * u;
+    h[i] = prompt_swiglu(g, u);
 }
 
 template <typename F>
@@ -824,10 +885,10 @@ TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
     // the f16-MFMA tiles where the shape fits them (rows in multiples of 64), else the row-dot kernel
     if (p->w_cols % kChunk == 0 && p->w_rows % 64 == 0 && p->n <= kMaxExpertsMmq && aligned(p->w, 16) &&
         p->expert_bytes % 16 == 0) {
-        const int64_t max_tiles = (p->total_rows + kBN - 1) / kBN + p->n;
         const int nw = p->w_rows % 256 == 0 ? 8 : p->w_rows % 128 == 0 ? 4 : 2;
         return with_type(p->type, [&](auto T) {
             constexpr int TT = decltype(T)::value;
+            const int64_t max_tiles = (p->total_rows + bn_of<TT>() - 1) / bn_of<TT>() + p->n;
             const dim3 grid((unsigned) (p->w_rows / (32 * nw)), (unsigned) max_tiles);
             const uint8_t* w = (const uint8_t*) p->w;
             if (nw == 8)
@@ -873,8 +934,9 @@ TSX_API int tsx_moe_mmq_gate_up_swiglu(const void* w, int type, int64_t n_ff, in
     if (n_exp == 0 || n_rows == 0) return TSX_OK;
     const MmqPlanes P = planes((void*) xq, x_rows, n_embd), H = planes(hq, n_rows, n_ff);
     const hipStream_t s = (hipStream_t) stream;
-    const int64_t max_tiles = (n_rows + kBN - 1) / kBN + n_exp;
     return with_type(type, [&](auto T) {
+        constexpr int BN = bn_of<decltype(T)::value>();
+        const int64_t max_tiles = (n_rows + BN - 1) / BN + n_exp;
         const dim3 grid((unsigned) (n_ff / 128), (unsigned) max_tiles);
         mmq_f16_kernel<decltype(T)::value, 8, true><<<grid, 512, 0, s>>>(
             (const uint8_t*) w, expert_bytes, rb, (int) n_embd, n_exp, P, bounds, nullptr, nullptr, 0, xids, H, (int) n_ff);
