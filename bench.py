@@ -7,7 +7,8 @@ Default: the decode MoE layer stack of BASELINE.json configs[1].  A step is one 
                             HBM): routing, grouping, Q8_1 activations, the grouped experts (and the shared expert) and
                             the weighted combine, each layer's output feeding the next (x <- x + moe(x)).
   prefill / prefill_long    a prompt chunk (512 or 4096 tokens) through 4 such layers with the prompt path: routing,
-                            expert sort, gathered Q8_1 activations, int8-MFMA grouped gate/up, SwiGLU, down, combine.
+                            expert sort, Q8_1 activations, the grouped gate/up with SwiGLU (f16 MFMA on exact integer
+                            codes), the grouped down product and the combine.
 Inputs are synthetic (N(0,0.02) weights quantized by this library, N(0,1) activations, N(0,1) router logits with the
 config's skew) and resident in HBM before the timed region.  Prints one JSON line: the driver's contract plus the
 roofline of the dominant launch (timed with HIP events on its stream) and the reference CPU path timed on this host.
@@ -268,7 +269,8 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None):
                                      ml.lscratch, shared=ml.W.shared, sgate=sg_d[l] if shared else None)
         dom_bytes = float(np.mean(layer_bytes))
         dom_ops = float(layer_ops)
-        kernel = "tsx_moe_decode_layer (layer_gu_kernel + layer_down_kernel) per layer"
+        kernel = ("tsx_moe_decode_layer (" + ("layer_gu1_kernel" if T == 1 else "layer_gu_kernel") +
+                  " + layer_down_kernel) per layer")
     dom()
     torch.cuda.synchronize()
     # replayed from a HIP graph like the timed steps, so the figure is the kernels' time, not host launch gaps
