@@ -81,6 +81,7 @@ class MoELayer:
     def __init__(self, W: MoEWeights, k: int, n_tok: int, device: torch.device, decode_max: int = 8,
                  fused: bool = True):
         self.W, self.k, self.n_tok = W, k, n_tok
+        self.side = None  # the prompt path's second stream (the shared expert), made on first use
         L = W.L
         self.N, self.FF = int(L.n_embd), int(L.n_ff)
         self.decode = n_tok <= decode_max
@@ -194,12 +195,23 @@ class MoELayer:
     def _prefill_fused(self, x, sgate, y, bounds, et, rinv):
         W, L, k, N, FF, T = self.W, self.W.L, self.k, self.N, self.FF, self.n_tok
         ops.mmq_quantize(x, None, L.gu_type, N, N, T, xq=self.txq)  # every token once; routed rows read it via et
+        main = torch.cuda.current_stream()
+        if W.shared is not None:
+            # the shared expert's two products on a second stream, alongside the routed ones: its 4 x ceil(T / 128)
+            # blocks fill the CUs the routed launches leave idle (their last round of blocks)
+            if self.side is None:
+                self.side = torch.cuda.Stream(device=x.device)
+            self.side.wait_stream(main)
+            with torch.cuda.stream(self.side):
+                sh = W.shared
+                ops.mmq_gate_up_swiglu(sh, L.gu_type, FF, N, W.stride, 1, self.txq, T, None, self.sh_bounds, T,
+                                       hq=self.shq)
+                ops.mmq_run(sh[L.down_off:], L.d_type, N, FF, W.stride, 1, self.shq, self.sh_bounds, None, T, self.sh,
+                            N)
         ops.mmq_gate_up_swiglu(W.blobs, L.gu_type, FF, N, W.stride, W.n_expert, self.txq, T, et, bounds, self.n_ent,
                                hq=self.mhq)
         ops.mmq_run(W.blobs[L.down_off:], L.d_type, N, FF, W.stride, W.n_expert, self.mhq, bounds, None, self.n_ent,
                     self.parts, N)
         if W.shared is not None:
-            sh = W.shared
-            ops.mmq_gate_up_swiglu(sh, L.gu_type, FF, N, W.stride, 1, self.txq, T, None, self.sh_bounds, T, hq=self.shq)
-            ops.mmq_run(sh[L.down_off:], L.d_type, N, FF, W.stride, 1, self.shq, self.sh_bounds, None, T, self.sh, N)
+            main.wait_stream(self.side)
         self._combine(y, sgate, prow=rinv)
