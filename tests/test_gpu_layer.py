@@ -248,3 +248,35 @@ def test_moe_block_norm(cfg, fused):
     print(f"{cfg}: h against the closed-form norm: max error {err:.2e} of max |h|")
     assert err < 2e-6
     assert (hqv == O.quantize_q8_1(hv)).all()
+
+
+def test_prompt_layer_graph_replay():
+    """A prompt chunk's layer (the shared expert's products on a second stream) captured in a graph replays to the
+    eager call's bits, every time, with eager work and synchronisations between the replays."""
+    gu, d, N, FF, E, k, shared, T = CONFIGS["c5_prefill_iq3_16tok"]
+    T = 300
+    L, p, order, W = make_layer(gu, d, N, FF, E, shared)
+    x, logits, sgate = inputs("c5", T, E, N, seed=17)
+    layer = moe.MoELayer(W, k, T, torch.device("cuda"))
+    xd, ld, sd = dev(x), dev(logits), dev(sgate)
+    y = torch.zeros((T, N), device="cuda")
+    layer(xd, ld, sd, y)
+    eager = host(y)
+    ref, _, _ = O.moe_layer(0, O.layout(gu, d, N, FF), x[:8], logits[:8], k, p[order], p.shape[1], p[len(p) - 1],
+                            sgate[:8])
+    assert rel_l2(eager[:8], ref) < 1e-3
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        y.zero_()
+        layer(xd, ld, sd, y)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y.zero_()
+        layer(xd, ld, sd, y)
+    for _ in range(3):
+        g.replay()
+        assert (host(y) == eager).all()
+        y.fill_(7.0)
+        torch.cuda.synchronize()
