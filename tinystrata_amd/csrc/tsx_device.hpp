@@ -460,9 +460,26 @@ struct OpAdd {
 __device__ __forceinline__ float q8_1_finite(float v) { return fabsf(v) > 65504.0f ? copysignf(65504.0f, v) : v; }
 // The Q8_1 code of v in a block of scale d = q8_1_finite(amax / 127) (amax the block's largest magnitude):
 // roundf(v / d) clamped to [-127, 127], 0 when amax is 0 - the reference quantizer's code, bit for bit.  rd = 1 / d is
-// the correctly rounded reciprocal (one IEEE division per block); the quotient is Markstein's corrected product
+// the correctly rounded reciprocal (q8_1_rcp, once per block); the quotient is Markstein's corrected product
 // q = v rd, r = v - d q (exact by fma), q + r rd, which is the correctly rounded v / d when rd is and nothing under- or
 // overflows (d >= 2^-100; a smaller d takes the division).  roundf ties away from zero; the clamp is one v_med3.
+// d = q8_1_finite(amax / 127) without a division: Markstein's corrected product with the correctly rounded
+// reciprocal of 127, which equals the IEEE quotient for every non-negative finite float (checked exhaustively)
+__device__ __forceinline__ float q8_1_scale(float amax) {
+    constexpr float R = 1.0f / 127.0f;
+    const float q0 = amax * R;
+    return q8_1_finite(__builtin_fmaf(__builtin_fmaf(-127.0f, q0, amax), R, q0));
+}
+// 1 / d correctly rounded, for q8_1_code_rd: in [2^-100, 2^100] the hardware reciprocal and one fma Newton step,
+// which equal the IEEE quotient for every float of that range (checked exhaustively on gfx950); elsewhere (q8_1_code_rd
+// divides there instead) the IEEE quotient
+__device__ __forceinline__ float q8_1_rcp(float d) {
+    if (d >= 0x1p-100f && d <= 0x1p100f) {
+        const float r0 = __builtin_amdgcn_rcpf(d);
+        return __builtin_fmaf(__builtin_fmaf(-d, r0, 1.0f), r0, r0);
+    }
+    return 1.0f / d;
+}
 __device__ __forceinline__ int q8_1_code_rd(float v, float amax, float d, float rd) {
     if (amax == 0.0f) return 0;
     float z;
@@ -483,8 +500,8 @@ __device__ __forceinline__ void q8_1_store32(float x, tsx_block_q8_1* y, int i) 
         amax = fmaxf(amax, __shfl_xor(amax, o, 32));
         sum += __shfl_xor(sum, o, 32);
     }
-    const float d = q8_1_finite(amax / 127.0f);
-    y->qs[i] = (int8_t) q8_1_code_rd(x, amax, d, 1.0f / d);
+    const float d = q8_1_scale(amax);
+    y->qs[i] = (int8_t) q8_1_code_rd(x, amax, d, q8_1_rcp(d));
     if (i == 0) {
         y->d = f2h(q8_1_finite(d));
         y->s = f2h(q8_1_finite(sum));

@@ -120,7 +120,7 @@ __device__ __forceinline__ void act_planes(const int8_t* codes, const float* d, 
 __device__ __forceinline__ void q8_1_quad_to_lds(const float4& x, bool valid, int8_t* codes, float* d, int l8) {
     float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
     amax = lanes_reduce<8>(amax, OpMax());
-    const float dd = q8_1_finite(amax / 127.0f), rd = 1.0f / dd;
+    const float dd = q8_1_scale(amax), rd = q8_1_rcp(dd);
     const uint32_t packed = ((uint32_t) q8_1_code_rd(x.x, amax, dd, rd) & 0xFFu) |
                             ((uint32_t) q8_1_code_rd(x.y, amax, dd, rd) & 0xFFu) << 8 |
                             ((uint32_t) q8_1_code_rd(x.z, amax, dd, rd) & 0xFFu) << 16 |
@@ -366,10 +366,10 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu_kernel(LayerArgs a) {
             const float gt = s_gu[e][i];
             const float h = (gt / (1.0f + expf(-gt))) * s_gu[e][kSliceA + i];
             const float amax = lanes_reduce<32>(fabsf(h), OpMax());
-            const float dd = q8_1_finite(amax / 127.0f);
+            const float dd = q8_1_scale(amax);
             if ((tid >> 5) < n_e) {
                 const int64_t p = p0 + e;
-                a.hc[p * FF + kSliceA * cur.j + i] = (int8_t) q8_1_code_rd(h, amax, dd, 1.0f / dd);
+                a.hc[p * FF + kSliceA * cur.j + i] = (int8_t) q8_1_code_rd(h, amax, dd, q8_1_rcp(dd));
                 if (i == 0) a.hd[p * (FF / 32) + cur.j] = h2f(f2h(dd));
             }
         }
@@ -554,7 +554,6 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ LayerTables s_tab;
     __shared__ float s_part[kMaxEnt + kMaxTok][kRowsB];
-    __shared__ const uint8_t* s_gsrc[kMaxEnt + 1];
     __shared__ float s_sgate[kMaxTok];
 
     const int tid = threadIdx.x;
@@ -584,10 +583,12 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     __syncthreads();
     const int ng = s_tab.n_groups;
     const int G = ng + (a.shared ? 1 : 0);  // group ng is the shared expert: positions [n_ent, n_ent + T)
-    if (tid < G)  // where each group's 8 down rows start
-        s_gsrc[tid] = (tid < ng ? a.blobs + (uint64_t) s_tab.grp_expert[tid] * a.stride : a.shared) + L.down_off +
-                      (uint64_t) r0 * d_row;
-    __syncthreads();
+    // where group g's 8 down rows start (group ng is the shared expert), read by each thread from the tables: no
+    // block barrier between the tables and the row loads
+    auto gsrc = [&](int g) {
+        return (g < ng ? a.blobs + (uint64_t) s_tab.grp_expert[g] * a.stride : a.shared) + L.down_off +
+               (uint64_t) r0 * d_row;
+    };
     auto grp_lo = [&](int g) { return g < ng ? s_tab.grp_start[g] : n_ent; };
     auto grp_hi = [&](int g) { return g < ng ? s_tab.grp_start[g + 1] : n_ent + T; };
 
@@ -601,7 +602,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
 #pragma unroll
         for (int i = 0; i < kBLoads; ++i) {  // unconditional (clamped) loads keep the wait counts exact
             const int q = min(tid + kThreadsB * i, np - 1), g = div_small(q, ppg, rppg), pp = q - g * ppg;
-            reg[i] = __builtin_nontemporal_load(gbl_at<v4i>((uintptr_t) s_gsrc[g0 + g]) + pp);
+            reg[i] = __builtin_nontemporal_load(gbl_at<v4i>((uintptr_t) gsrc(g0 + g)) + pp);
         }
     };
     issue(0);
@@ -613,14 +614,16 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     int8_t* s_hq = (int8_t*) (smem + a.slab_b + rep_lds_bytes<DT>());
     float* s_hd = (float*) (s_hq + (size_t) P * FF);
     if (a.h_fp32) {  // every Q8_1 block of h from its eight quads (consecutive lanes), as launch A would write it
-        // (the loop conditions are the same in every thread: whole waves take part in each block's reduction)
+        // (the conditions are the same in every lane of a wave: whole waves take part in each block's reduction,
+        // and a wave with no quad left skips the round)
+        const int w0 = tid & ~63;
 #pragma unroll
         for (int i = 0; i < kHLoads; ++i) {
             const int q = tid + kThreadsB * i;
-            if (kThreadsB * i < nh)
+            if (kThreadsB * i + w0 < nh)
                 q8_1_quad_to_lds(__builtin_bit_cast(float4, hv[i]), q < nh, s_hq + 4 * q, s_hd + q / 8, tid & 7);
         }
-        for (int base = kThreadsB * kHLoads; base < nh; base += kThreadsB) {
+        for (int base = kThreadsB * kHLoads; base + w0 < nh; base += kThreadsB) {
             const int q = base + tid;
             q8_1_quad_to_lds(__builtin_bit_cast(float4, hsrc[min(q, nh - 1)]), q < nh, s_hq + 4 * q, s_hd + q / 8,
                              tid & 7);
@@ -644,7 +647,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
             if (tid + kThreadsB * i < np) slab[tid + kThreadsB * i] = reg[i];
         for (int q = tid + kThreadsB * kBLoads; q < np; q += kThreadsB) {  // a chunk larger than the loads in flight
             const int g = q / ppg, pp = q - g * ppg;
-            slab[q] = gbl_at<v4i>((uintptr_t) s_gsrc[g0 + g])[pp];
+            slab[q] = gbl_at<v4i>((uintptr_t) gsrc(g0 + g))[pp];
         }
         __syncthreads();  // the chunk (and h, the codebooks) are in LDS
         if (ch + 1 < nchunks) issue(ch + 1);

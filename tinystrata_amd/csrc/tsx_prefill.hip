@@ -73,7 +73,7 @@ __global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __r
     const float4 v = *(const float4*) (x + src * ld + 4 * c4);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = lanes_reduce<8>(amax, OpMax());
-    const float d = q8_1_finite(amax / 127.0f), rd = 1.0f / d;
+    const float d = q8_1_scale(amax), rd = q8_1_rcp(d);
     auto code = [&](float f) { return q8_1_code_rd(f, amax, d, rd); };
     const int q0 = code(v.x), q1 = code(v.y), q2 = code(v.z), q3 = code(v.w);
     const float qs = lanes_reduce<8>((float) (q0 + q1 + q2 + q3), OpAddF());  // |sum| <= 32 * 127: exact in fp32
@@ -106,8 +106,8 @@ __global__ void __launch_bounds__(kThreads) mmq_quantize1_kernel(const float* __
     float amax = fabsf(v);
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-    const float d = q8_1_finite(amax / 127.0f);
-    const int q = q8_1_code_rd(v, amax, d, 1.0f / d);
+    const float d = q8_1_scale(amax);
+    const int q = q8_1_code_rd(v, amax, d, q8_1_rcp(d));
     int qs = q;
 #pragma unroll
     for (int o = 16; o > 0; o >>= 1) qs += __shfl_xor(qs, o, 32);
@@ -758,7 +758,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     for (int k = 0; k < 4; ++k) hv[k] = prompt_swiglu(gp[k], gp[BM / 2 + k]);
                     float amax = fmaxf(fmaxf(fabsf(hv[0]), fabsf(hv[1])), fmaxf(fabsf(hv[2]), fabsf(hv[3])));
                     amax = lanes_reduce<8>(amax, OpMax());
-                    const float d = q8_1_finite(amax / 127.0f), rd = 1.0f / d;
+                    const float d = q8_1_scale(amax), rd = q8_1_rcp(d);
                     int qv[4];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) qv[k] = q8_1_code_rd(hv[k], amax, d, rd);
