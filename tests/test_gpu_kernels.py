@@ -29,12 +29,9 @@ def test_quantize_q8_1_bytes_exact():
     assert (got == O.quantize_q8_1(x)).all()
 
 
-def test_quantize_q8_1_halves_exact():
-    """Quotients on and next to half-integers, where a quotient one ulp off would change roundf's code: the GPU forms
-    v / d as a corrected product of the reciprocal, which must give the reference's codes (IEEE division, roundf) for
-    every one of them, across block scales from subnormal-adjacent to the fp16 clamp."""
-    rng = np.random.default_rng(11)
-    rows, nb = 4096, 8
+def _halves_rows(rng, rows, nb):
+    """Rows of nb Q8_1 blocks whose values sit on and a few ulps beside half-integer multiples of the block scale, with
+    block scales log-uniform from subnormal-adjacent to the fp16 clamp (so about one block in five has d < 2^-100)."""
     amax = np.exp(rng.uniform(np.log(1e-36), np.log(1e7), (rows, nb))).astype(np.float32)
     d = np.minimum(amax / np.float32(127.0), np.float32(65504.0)).astype(np.float32)
     n = rng.integers(-127, 127, (rows, nb, 31)).astype(np.float32)
@@ -47,8 +44,35 @@ def test_quantize_q8_1_halves_exact():
     x = np.concatenate([amax[..., None], vals], axis=2)             # the block's amax first
     x = np.where(rng.random(x.shape) < 0.5, -x, x).astype(np.float32).reshape(rows, nb * 32)
     assert np.isfinite(x).all()
+    return x
+
+
+def test_quantize_q8_1_halves_exact():
+    """Quotients on and next to half-integers, where a quotient one ulp off would change roundf's code: the GPU forms
+    v / d as a corrected product of the reciprocal, which must give the reference's codes (IEEE division, roundf) for
+    every one of them, across block scales from subnormal-adjacent to the fp16 clamp."""
+    x = _halves_rows(np.random.default_rng(11), 4096, 8)
     got = host(ops.quantize_q8_1_rows(dev(x)))
     assert (got == O.quantize_q8_1(x)).all()
+
+
+def test_mmq_quantize_halves_exact():
+    """The prompt quantizer's four-values-per-lane path on the same quotients: waves whose blocks all have d in
+    [2^-100, 2^100] take the straight corrected products, waves holding a smaller d take the per-value path; both
+    must give the reference's codes and scales, and the sums of the codes.  Zero blocks sit among them."""
+    rng = np.random.default_rng(12)
+    x = _halves_rows(rng, 2048, 8)
+    x[::7, 64:96] = 0.0
+    rows, cols = x.shape
+    xq = host(ops.mmq_quantize(dev(x), None, Q4_K, cols, cols, rows))
+    rp = (rows + 63) // 64 * 64 + 64
+    r256 = lambda v: (v + 255) // 256 * 256
+    q = xq[: rows * cols].view(np.int8).reshape(-1, 32)
+    d = xq[r256(rp * cols): r256(rp * cols) + rows * cols // 32 * 4].view(np.float32)
+    m0 = r256(rp * cols) + r256(rp * cols // 32 * 4)
+    m = xq[m0: m0 + rows * cols // 32 * 4].view(np.int32)
+    ed, _, ecodes = O.q8_1_split(O.quantize_q8_1(x))
+    assert (q == ecodes).all() and (d == ed).all() and (m == ecodes.astype(np.int32).sum(1)).all()
 
 
 @pytest.mark.parametrize("t", TYPES)

@@ -480,6 +480,11 @@ __device__ __forceinline__ float q8_1_rcp(float d) {
     }
     return 1.0f / d;
 }
+__device__ __forceinline__ int q8_1_round_clamp(float z) {  // roundf (ties away from zero), clamped to [-127, 127]
+    const float t = __builtin_truncf(z);
+    const float r = t + (__builtin_fabsf(z - t) >= 0.5f ? __builtin_copysignf(1.0f, z) : 0.0f);
+    return (int) __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
+}
 __device__ __forceinline__ int q8_1_code_rd(float v, float amax, float d, float rd) {
     if (amax == 0.0f) return 0;
     float z;
@@ -489,9 +494,28 @@ __device__ __forceinline__ int q8_1_code_rd(float v, float amax, float d, float 
     } else {
         z = v / d;
     }
-    const float t = __builtin_truncf(z);
-    const float r = t + (__builtin_fabsf(z - t) >= 0.5f ? __builtin_copysignf(1.0f, z) : 0.0f);
-    return (int) __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
+    return q8_1_round_clamp(z);
+}
+// q8_1_code_rd's four codes of one lane's quad (block scale d of block amax), with one wave-uniform branch: when every
+// block of the wave with a nonzero amax has d in [2^-100, 2^100] (where q8_1_rcp is the corrected reciprocal), the
+// corrected products run straight through for every lane (a zero block's codes are 0: its reciprocal is never used);
+// otherwise each value takes q8_1_code_rd.  Call with every lane of the wave.
+__device__ __forceinline__ void q8_1_codes4(const float4& x, float amax, float d, int (&q)[4]) {
+    const float v[4] = {x.x, x.y, x.z, x.w};
+    if (__builtin_amdgcn_ballot_w64(amax != 0.0f && !(d >= 0x1p-100f && d <= 0x1p100f)) == 0) {
+        const float r0 = __builtin_amdgcn_rcpf(d);
+        const float rd = __builtin_fmaf(__builtin_fmaf(-d, r0, 1.0f), r0, r0);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float p = v[k] * rd;
+            const int c = q8_1_round_clamp(__builtin_fmaf(__builtin_fmaf(-d, p, v[k]), rd, p));
+            q[k] = amax == 0.0f ? 0 : c;
+        }
+    } else {
+        const float rd = q8_1_rcp(d);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = q8_1_code_rd(v[k], amax, d, rd);
+    }
 }
 __device__ __forceinline__ void q8_1_store32(float x, tsx_block_q8_1* y, int i) {
     float amax = fabsf(x), sum = x;

@@ -120,11 +120,11 @@ __device__ __forceinline__ void act_planes(const int8_t* codes, const float* d, 
 __device__ __forceinline__ void q8_1_quad_to_lds(const float4& x, bool valid, int8_t* codes, float* d, int l8) {
     float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
     amax = lanes_reduce<8>(amax, OpMax());
-    const float dd = q8_1_scale(amax), rd = q8_1_rcp(dd);
-    const uint32_t packed = ((uint32_t) q8_1_code_rd(x.x, amax, dd, rd) & 0xFFu) |
-                            ((uint32_t) q8_1_code_rd(x.y, amax, dd, rd) & 0xFFu) << 8 |
-                            ((uint32_t) q8_1_code_rd(x.z, amax, dd, rd) & 0xFFu) << 16 |
-                            ((uint32_t) q8_1_code_rd(x.w, amax, dd, rd) & 0xFFu) << 24;
+    const float dd = q8_1_scale(amax);
+    int c[4];
+    q8_1_codes4(x, amax, dd, c);
+    const uint32_t packed = ((uint32_t) c[0] & 0xFFu) | ((uint32_t) c[1] & 0xFFu) << 8 |
+                            ((uint32_t) c[2] & 0xFFu) << 16 | ((uint32_t) c[3] & 0xFFu) << 24;
     if (valid) {
         *(uint32_t*) codes = packed;
         if (l8 == 0) *d = h2f(f2h(dd));
@@ -667,15 +667,16 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
                 rr[m] = ri % kRowsB;
                 pos[m] = grp_lo(g0 + g);
                 v[m] = 0.f;
-                if (kThreadsB * m < items)  // the same in every thread
-                    unit_load<DT>((const uint8_t*) smem + g * gb + rr[m] * d_row, u, w[m], grid);
+                if (kThreadsB * m < items)  // the same in every thread (24-bit products: full-rate multiplies)
+                    unit_load<DT>((const uint8_t*) smem + __umul24(g, gb) + __umul24(rr[m], (uint32_t) d_row), u, w[m],
+                                  grid);
             }
 #pragma unroll
             for (int m = 0; m < kItemsB1; ++m) {
                 if (kThreadsB * m < items) {
                     const int it = min(tid + kThreadsB * m, items - 1), u = it & (NUd - 1);
                     Act xa;
-                    act_planes(s_hq + (size_t) pos[m] * FF + 32 * u, s_hd + pos[m] * NUd + u, xa);
+                    act_planes(s_hq + __umul24(pos[m], FF) + 32 * u, s_hd + (pos[m] << lgu) + u, xa);
                     int S, M;
                     v[m] = unit_dot<DT>(w[m], xa, S, M);
                 }

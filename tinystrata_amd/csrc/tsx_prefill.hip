@@ -73,9 +73,10 @@ __global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __r
     const float4 v = *(const float4*) (x + src * ld + 4 * c4);
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     amax = lanes_reduce<8>(amax, OpMax());
-    const float d = q8_1_scale(amax), rd = q8_1_rcp(d);
-    auto code = [&](float f) { return q8_1_code_rd(f, amax, d, rd); };
-    const int q0 = code(v.x), q1 = code(v.y), q2 = code(v.z), q3 = code(v.w);
+    const float d = q8_1_scale(amax);
+    int qv[4];
+    q8_1_codes4(v, amax, d, qv);
+    const int q0 = qv[0], q1 = qv[1], q2 = qv[2], q3 = qv[3];
     const float qs = lanes_reduce<8>((float) (q0 + q1 + q2 + q3), OpAddF());  // |sum| <= 32 * 127: exact in fp32
     if (valid) {
         *(uint32_t*) (P.q + i * cols + 4 * c4) = ((uint32_t) q0 & 0xFFu) | ((uint32_t) q1 & 0xFFu) << 8 |
@@ -758,10 +759,9 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     for (int k = 0; k < 4; ++k) hv[k] = prompt_swiglu(gp[k], gp[BM / 2 + k]);
                     float amax = fmaxf(fmaxf(fabsf(hv[0]), fabsf(hv[1])), fmaxf(fabsf(hv[2]), fabsf(hv[3])));
                     amax = lanes_reduce<8>(amax, OpMax());
-                    const float d = q8_1_scale(amax), rd = q8_1_rcp(d);
+                    const float d = q8_1_scale(amax);
                     int qv[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) qv[k] = q8_1_code_rd(hv[k], amax, d, rd);
+                    q8_1_codes4(float4{hv[0], hv[1], hv[2], hv[3]}, amax, d, qv);
                     const float qs = lanes_reduce<8>((float) (qv[0] + qv[1] + qv[2] + qv[3]), OpAddF());
                     if (t0 + tok < nrows) {
                         const int64_t hr = row0 + t0 + tok, col = (int64_t) (BM / 2) * bx + 4 * f4;
