@@ -269,7 +269,7 @@ template <int T, int NW, int NB> struct F16Layout {
     static constexpr int BN = bn_of<T>();
     static constexpr int DL = RHO + lds_round(NB * BN * 8 * 4);
     static constexpr int DM = DL + lds_round(BN * 4);
-    static constexpr int SCAN = DM + lds_round((Q4K ? NB * BN : 1) * 8 * 4);
+    static constexpr int SCAN = DM + lds_round((Q4K ? NB * 8 * (BN + 16) : 1) * 4);
     static constexpr int RAW = SCAN + lds_round((NW + 2) * 4);
     static constexpr int TB = RAW + lds_round(NW * 32 * raw_stride<T>());
     static constexpr int BYTES = TB + NB * BN * kBStride * 2;
@@ -355,9 +355,12 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     auto& s_uf = *reinterpret_cast<float(*)[Q4K || Q80 ? NW : 1][8][32]>(s_lds + L::UF);  // Q4_K: dmin m / w'; Q8_0: ratio
     auto& s_rw = *reinterpret_cast<float(*)[NW][32]>(s_lds + L::RW);  // row ratio at the chunk's first unit
     auto& s_dw = *reinterpret_cast<float(*)[NW][32]>(s_lds + L::DW);  // the row's scale w' so far
-    auto& s_rho = *reinterpret_cast<float(*)[NB][kBN][8]>(s_lds + L::RHO);  // token ratio per unit
+    // per-token factors are unit-major (token index fastest), so that the 16 tokens of a fragment read 16 banks
+    auto& s_rho = *reinterpret_cast<float(*)[NB][8][kBN]>(s_lds + L::RHO);  // token ratio per unit
     float* const s_dl = reinterpret_cast<float*>(s_lds + L::DL);             // the token's D' so far
-    auto& s_dm = *reinterpret_cast<float(*)[Q4K ? NB : 1][Q4K ? kBN : 1][8]>(s_lds + L::DM);
+    // Q4_K min-term factors: rows of kBN + 16 floats, so that lane groups 0 and 1 (units 4 h, 4 h + 1) of one
+    // 32-lane half read different banks
+    auto& s_dm = *reinterpret_cast<float(*)[Q4K ? NB : 1][8][Q4K ? kBN + 16 : 1]>(s_lds + L::DM);
     int* const s_scan = reinterpret_cast<int*>(s_lds + L::SCAN);
     int& s_x = s_scan[NW];
     int& s_tile0 = s_scan[NW + 1];
@@ -471,18 +474,16 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                 prev = dn;
             }
             s_dl[tid] = prev;
-            float4* rp = (float4*) s_rho[buf][tid];
-            rp[0] = float4{rho[0], rho[1], rho[2], rho[3]};
-            rp[1] = float4{rho[4], rho[5], rho[6], rho[7]};
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s_rho[buf][u][tid] = rho[u];
             if constexpr (Q4K) {
                 const int m8[8] = {am4[0].x, am4[0].y, am4[0].z, am4[0].w, am4[1].x, am4[1].y, am4[1].z, am4[1].w};
                 float mf[8];
                 const float rp = 1.0f / prev;
 #pragma unroll
                 for (int u = 0; u < 8; ++u) mf[u] = d8[u] * (float) m8[u] * rp;
-                float4* mq = (float4*) s_dm[buf][tid];
-                mq[0] = float4{mf[0], mf[1], mf[2], mf[3]};
-                mq[1] = float4{mf[4], mf[5], mf[6], mf[7]};
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s_dm[buf][u][tid] = mf[u];
             }
             (void) dn8;
         }
@@ -665,7 +666,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
 #pragma unroll
                 for (int tj = 0; tj < NTT; ++tj) {
                     const v4i bf = bq[(tj * 16 * kBStride + 32 * u) / 8];
-                    const float rh = s_rho[buf][16 * tj + lr][u];
+                    const float rh = s_rho[buf][u][16 * tj + lr];
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
                         v4f C;
@@ -697,7 +698,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     for (int t = 0; t < 2; ++t) am[t] = -s_uf[wave][4 * h + g][16 * t + lr];
 #pragma unroll
                     for (int tj = 0; tj < NTT; ++tj) {
-                        const float bm = s_dm[buf][16 * tj + lr][4 * h + g];
+                        const float bm = s_dm[buf][4 * h + g][16 * tj + lr];
 #pragma unroll
                         for (int t = 0; t < 2; ++t) {
                             const v4f C = {acc[t][tj][0], acc[t][tj][1], acc[t][tj][2], acc[t][tj][3]};
