@@ -169,9 +169,9 @@ __global__ void __launch_bounds__(kThreads) mmq_rows_kernel(const uint8_t* __res
 }
 
 // ------------------------------------------------------------------ grouped product (f16 MFMA, exact unit sums)
-// Block (weight-row tile bx, token tile by): BM = 32 * NW rows of one expert's matrix against up to 64 of the
-// expert's sorted token rows.  The token tiles of all experts are numbered in expert order (tiles of expert x =
-// ceil(rows_x / 64)); each block finds its expert from `bounds` with a block scan, so the launch needs no host-side
+// Block (weight-row tile bx, token tile by): BM = 32 * NW rows of one expert's matrix against up to kBN of the
+// expert's sorted token rows.  The token tiles are numbered full tiles first (expert order), then each expert's
+// partial last tile; each block finds its expert from `bounds` with a block scan, so the launch needs no host-side
 // count.
 //
 // The product runs on v_mfma_f32_16x16x32_f16, one MFMA per 32-value unit, with operands that are small integers and
@@ -267,7 +267,8 @@ template <int T, int NW, int NB> struct F16Layout {
     static constexpr int DW = RW + lds_round(NW * 32 * 4);
     static constexpr int RHO = DW + lds_round(NW * 32 * 4);
     static constexpr int BN = bn_of<T>();
-    static constexpr int DL = RHO + lds_round(NB * BN * 8 * 4);
+    static constexpr int RS = BN / 16 == 8 ? 12 : BN / 16;  // floats per (unit, lane token) of the ratio array
+    static constexpr int DL = RHO + lds_round(NB * 8 * 16 * RS * 4);
     static constexpr int DM = DL + lds_round(BN * 4);
     static constexpr int SCAN = DM + lds_round((Q4K ? NB * 8 * (BN + 16) : 1) * 4);
     static constexpr int RAW = SCAN + lds_round((NW + 2) * 4);
@@ -355,8 +356,10 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     auto& s_uf = *reinterpret_cast<float(*)[Q4K || Q80 ? NW : 1][8][32]>(s_lds + L::UF);  // Q4_K: dmin m / w'; Q8_0: ratio
     auto& s_rw = *reinterpret_cast<float(*)[NW][32]>(s_lds + L::RW);  // row ratio at the chunk's first unit
     auto& s_dw = *reinterpret_cast<float(*)[NW][32]>(s_lds + L::DW);  // the row's scale w' so far
-    // per-token factors are unit-major (token index fastest), so that the 16 tokens of a fragment read 16 banks
-    auto& s_rho = *reinterpret_cast<float(*)[NB][8][kBN]>(s_lds + L::RHO);  // token ratio per unit
+    // token ratio per unit, [unit][token % 16][token / 16]: a lane reads the ratios of its 8 (4) tokens 16 apart
+    // with two (one) 16-byte reads, the 16 tokens of a lane group on distinct banks (rows of 12 floats when 8 are
+    // used)
+    auto& s_rho = *reinterpret_cast<float(*)[NB][8][16][L::RS]>(s_lds + L::RHO);
     float* const s_dl = reinterpret_cast<float*>(s_lds + L::DL);             // the token's D' so far
     // Q4_K min-term factors: rows of kBN + 16 floats, so that lane groups 0 and 1 (units 4 h, 4 h + 1) of one
     // 32-lane half read different banks
@@ -371,29 +374,37 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     const int bx = blockIdx.x, by = blockIdx.y;
     const int lr = lane & 15, g = lane >> 4;
 
-    // 1. which expert and which of its token tiles: EPT experts per thread, a block scan of tile counts
+    // 1. which expert and which of its token tiles: EPT experts per thread, a block scan of tile counts.  The full
+    // tiles of every expert are numbered first (expert order) and the partial last tiles after them, so that the
+    // hardware dispatches the long blocks first and the short ones fill the end of the launch.  Counts travel
+    // packed: full tiles in the low 16 bits, partial tiles in the high 16 (each total is at most 32768 / 64)
     int tc[EPT], mine = 0;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const int x = EPT * tid + e;
         const int b0 = bounds[min(x, n_exp)], b1 = bounds[min(x + 1, n_exp)];
-        tc[e] = x < n_exp ? (b1 - b0 + kBN - 1) / kBN : 0;
+        const int rows = x < n_exp ? b1 - b0 : 0;
+        tc[e] = rows / kBN | (rows % kBN != 0 ? 1 << 16 : 0);
         mine += tc[e];
     }
     int total;
     int start = block_scan<NT>(mine, s_scan, total);
-    if (by >= total) return;  // the whole block: fewer tiles than the grid's upper bound
+    const int nfull = total & 0xFFFF;
+    if (by >= nfull + (total >> 16)) return;  // the whole block: fewer tiles than the grid's upper bound
+    const bool part = by >= nfull;
+    const int want = part ? by - nfull : by;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-        if (start <= by && by < start + tc[e]) {
+        const int s0 = part ? start >> 16 : start & 0xFFFF, n = part ? tc[e] >> 16 : tc[e] & 0xFFFF;
+        if (s0 <= want && want < s0 + n) {
             s_x = EPT * tid + e;
-            s_tile0 = start;
+            s_tile0 = part ? tc[e] & 0xFFFF : want - s0;  // the tile's index within its expert
         }
         start += tc[e];
     }
     __syncthreads();
     const int x = s_x;
-    const int row0 = bounds[x] + (by - s_tile0) * kBN;
+    const int row0 = bounds[x] + s_tile0 * kBN;
     const int nrows = min(kBN, bounds[x + 1] - row0);
     const int ntt = (nrows + 15) >> 4;  // 16-token MFMA tiles with rows in them
     const int wrow = FUSE ? (wave < NW / 2 ? 0 : n_ff) + (BM / 2) * bx + 32 * (wave % (NW / 2)) : bx * BM + 32 * wave;
@@ -469,17 +480,17 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const float dn = d8[u] != 0.f ? d8[u] : prev;
-                rho[u] = prev / dn;
+                rho[u] = prev * __builtin_amdgcn_rcpf(dn);  // within 2 ulp: the ratios only need to chain
                 dn8[u] = dn;
                 prev = dn;
             }
             s_dl[tid] = prev;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) s_rho[buf][u][tid] = rho[u];
+            for (int u = 0; u < 8; ++u) s_rho[buf][u][tid & 15][tid >> 4] = rho[u];
             if constexpr (Q4K) {
                 const int m8[8] = {am4[0].x, am4[0].y, am4[0].z, am4[0].w, am4[1].x, am4[1].y, am4[1].z, am4[1].w};
                 float mf[8];
-                const float rp = 1.0f / prev;
+                const float rp = __builtin_amdgcn_rcpf(prev);
 #pragma unroll
                 for (int u = 0; u < 8; ++u) mf[u] = d8[u] * (float) m8[u] * rp;
 #pragma unroll
@@ -508,7 +519,6 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             if (tid + NT * k < TW) s_tab[tid + NT * k] = tw[k];
     }
     stage(0);
-    if (nchunks > 1) fetch(1);
     __syncthreads();
 
     // the chunk loop, specialised on the number of 16-token tiles that hold rows (no per-tile branches inside)
@@ -663,10 +673,16 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                         rr[t][3] = v.w;
                     }
                 }
+                float4 rv[(NTT + 3) / 4];
+#pragma unroll
+                for (int q = 0; q < (NTT + 3) / 4; ++q) rv[q] = *(const float4*) &s_rho[buf][u][lr][4 * q];
+                // the unit's products at raised wave priority, so that they issue back to back while the SIMD's
+                // other wave decodes
+                __builtin_amdgcn_s_setprio(1);
 #pragma unroll
                 for (int tj = 0; tj < NTT; ++tj) {
                     const v4i bf = bq[(tj * 16 * kBStride + 32 * u) / 8];
-                    const float rh = s_rho[buf][u][16 * tj + lr];
+                    const float rh = rv[tj >> 2][tj & 3];
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
                         v4f C;
@@ -678,10 +694,14 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                         for (int i = 0; i < 4; ++i) acc[t][tj][i] = D[i];
                     }
                 }
+                __builtin_amdgcn_s_setprio(0);
                 if (u + 1 < 8) decode(u + 1, A);
             };
             decode(0, A);
             step(0, std::integral_constant<bool, true>{});
+            // the next chunk's loads, issued behind the first unit's products rather than in a burst between
+            // barriers (the vector memory path takes ~0.7 us to accept a chunk's 72 KB)
+            if (c + 1 < nchunks) fetch(c + 1);
 #pragma unroll 1
             for (int u = 1; u < 8; ++u) {
                 if constexpr (Q80) step(u, std::integral_constant<bool, true>{});
@@ -713,7 +733,6 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                 if constexpr (NB == 1) __syncthreads();  // every wave is done with the single activation tile
                 wave_lds_order();                        // this wave is done with its raw slab and factor rows
                 stage(NB == 2 ? (c + 1) & 1 : 0);
-                if (c + 2 < nchunks) fetch(c + 2);
                 __syncthreads();
             }
         }
