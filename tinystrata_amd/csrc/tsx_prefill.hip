@@ -331,8 +331,9 @@ __device__ __forceinline__ int block_scan(int v, int* s_wave, int& total) {
     return off + inc - v;
 }
 
-// FUSE: the gate/up product with SwiGLU and the Q8_1 of h fused in (NW = 8).  Block bx takes gate rows
-// [128 bx, 128 bx + 128) in waves 0-3 and the matching up rows (n_ff further) in waves 4-7; the activation rows are
+// FUSE: the gate/up product with SwiGLU and the Q8_1 of h fused in (NW = 8).  Block bx takes h columns
+// [128 bx, 128 bx + 128): wave w multiplies gate rows 128 bx + 16 w + [0, 16) (its first 16-row tile) and the up
+// rows n_ff further (its second), so that each lane holds matching gate and up outputs; the activation rows are
 // xids[sorted row] of P (sorted row r itself when xids is null); h leaves as Q8_1 planes H, one row per sorted row.
 template <int T, int NW, bool FUSE = false>
 __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restrict__ w, uint64_t expert_bytes,
@@ -407,8 +408,12 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     const int row0 = bounds[x] + s_tile0 * kBN;
     const int nrows = min(kBN, bounds[x + 1] - row0);
     const int ntt = (nrows + 15) >> 4;  // 16-token MFMA tiles with rows in them
-    const int wrow = FUSE ? (wave < NW / 2 ? 0 : n_ff) + (BM / 2) * bx + 32 * (wave % (NW / 2)) : bx * BM + 32 * wave;
+    const int wrow = FUSE ? (BM / 2) * bx + 16 * wave : bx * BM + 32 * wave;
     const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) wrow * row_bytes;
+    // byte offset of the wave's row r (0-31) from wbase: FUSE rows 16-31 are the up rows of rows 0-15
+    auto roff = [&](int r) -> uint64_t {
+        return FUSE ? (uint64_t) ((r & 15) + (r >= 16 ? n_ff : 0)) * row_bytes : (uint64_t) r * row_bytes;
+    };
     const int nu = w_cols / 32, nchunks = w_cols / kChunk;
     // the activation rows this thread loads (the same every chunk): rows past the tile's last take its last row
     int64_t arow_b[BP];
@@ -433,7 +438,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
             const int q = min(lane + 64 * i, 32 * PR - 1), r = q / PR, pc = q - r * PR;
-            const uint64_t o = (uint64_t) r * row_bytes + (uint64_t) c * CB;
+            const uint64_t o = roff(r) + (uint64_t) c * CB;
             const int need = (int) (((o & 15) + CB + 15) / 16);  // pieces that start before the block's end
             rw[i] = __builtin_nontemporal_load((const v4i*) (wbase + (o & ~(uint64_t) 15)) + min(pc, need - 1));
         }
@@ -541,7 +546,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             // units 4 hl .. 4 hl + 3); a zero row scale zeroes the row's weights for the chunk
             {
                 const int r = lane & 31, hl = lane >> 5;
-                const uint8_t* b = slab + r * RS + (int) (((uint64_t) r * row_bytes + (uint64_t) c * CB) & 15);
+                const uint8_t* b = slab + r * RS + (int) ((roff(r) + (uint64_t) c * CB) & 15);
                 const float wold = s_dw[wave][r];
                 if constexpr (T == TSX_IQ3_XXS || IQ3S || Q4K) {
                     const float d = h2f((uint16_t) ld16(b));
@@ -604,7 +609,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int r = 16 * t + lr;
-                blk[t] = slab + r * RS + (int) (((uint64_t) r * row_bytes + (uint64_t) c * CB) & 15);
+                blk[t] = slab + r * RS + (int) ((roff(r) + (uint64_t) c * CB) & 15);
             }
             // unit u's weight fragments (rows 16 t + lr, values 8 g .. 8 g + 7 of the unit)
             auto decode = [&](int u, v4i (&A)[2]) {
@@ -751,51 +756,56 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
 
         if constexpr (FUSE) {
 #pragma clang fp contract(off)
-            // the block's gate (columns 0-127) and up (128-255) outputs through LDS, in runs of TOK tokens: the
-            // activation tiles' LDS once every wave is past its last chunk
-            constexpr int OS = 2 * (BM / 2) + 1;  // floats per token: odd, so 16 tokens' writes hit distinct banks
-            constexpr int TOK = NB * kBN * kBStride * 2 >= kBN * OS * 4 ? kBN : kBN / 2;
-            float* so = (float*) &tB[0][0];
+            // h = silu(gate) * up in registers (lane: h columns 16 w + 4 g + i, tokens 16 tj + lr), the product
+            // rounded on its own, then its Q8_1 blocks.  A block's 32 columns are the 16 of waves 2 m and 2 m + 1:
+            // each reduces its half of the token's amax and code sum over its four lane groups and the halves meet
+            // in LDS (the activation tile's, once every wave is past its last chunk)
+            float* s_ex = (float*) &tB[0][0];  // [2][NW][16 NTT]: amax halves, then code-sum halves
+            constexpr int EX = 16 * NTT;
             __syncthreads();
-            for (int t0 = 0; t0 < 16 * NTT; t0 += TOK) {
+            float hv[NTT][4], am[NTT];
+#pragma unroll
+            for (int tj = 0; tj < NTT; ++tj) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) hv[tj][i] = prompt_swiglu(acc[0][tj][i], acc[1][tj][i]);
+                float a = fmaxf(fmaxf(fabsf(hv[tj][0]), fabsf(hv[tj][1])), fmaxf(fabsf(hv[tj][2]), fabsf(hv[tj][3])));
+                a = fmaxf(a, __shfl_xor(a, 16, 64));
+                a = fmaxf(a, __shfl_xor(a, 32, 64));
+                am[tj] = a;
+                if (g == 0) s_ex[wave * EX + 16 * tj + lr] = a;
+            }
+            __syncthreads();
+            float dd[NTT];
+            const int col = (BM / 2) * bx + 16 * wave + 4 * g;
+#pragma unroll
+            for (int tj = 0; tj < NTT; ++tj) {
+                const float amax = fmaxf(am[tj], s_ex[(wave ^ 1) * EX + 16 * tj + lr]);
+                const float d = q8_1_scale(amax);
+                int qv[4];
+                q8_1_codes4(float4{hv[tj][0], hv[tj][1], hv[tj][2], hv[tj][3]}, amax, d, qv);
+                float qs = (float) (qv[0] + qv[1] + qv[2] + qv[3]);  // |sum| <= 32 * 127: exact in fp32
+                qs += __shfl_xor(qs, 16, 64);
+                qs += __shfl_xor(qs, 32, 64);
+                if (g == 0) s_ex[NW * EX + wave * EX + 16 * tj + lr] = qs;
+                dd[tj] = d;
+                const int tok = 16 * tj + lr;
+                if (tok < nrows)
+                    *(uint32_t*) (H.q + (int64_t) (row0 + tok) * H.cols + col) =
+                        ((uint32_t) qv[0] & 0xFFu) | ((uint32_t) qv[1] & 0xFFu) << 8 | ((uint32_t) qv[2] & 0xFFu) << 16 |
+                        ((uint32_t) qv[3] & 0xFFu) << 24;
+            }
+            __syncthreads();
+            if ((wave & 1) == 0 && g == 0) {
 #pragma unroll
                 for (int tj = 0; tj < NTT; ++tj) {
-                    const int tok = 16 * tj + lr - t0;
-                    if (tok >= 0 && tok < TOK)
-#pragma unroll
-                        for (int t = 0; t < 2; ++t)
-#pragma unroll
-                            for (int i = 0; i < 4; ++i) so[tok * OS + 32 * wave + 16 * t + 4 * g + i] = acc[t][tj][i];
-                }
-                __syncthreads();
-                // h = silu(gate) * up (the product rounded on its own) and its Q8_1 blocks: 8 lanes per 32 values,
-                // 4 each, every lane taking part in the reductions
-                const int ntok = min(TOK, 16 * NTT - t0);  // a multiple of 16: whole rounds of the block
-                for (int q0 = 0; q0 < ntok * (BM / 8); q0 += NT) {
-                    const int q = q0 + tid, tok = q / (BM / 8), f4 = q % (BM / 8);
-                    const float* gp = so + tok * OS + 4 * f4;
-                    float hv[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) hv[k] = prompt_swiglu(gp[k], gp[BM / 2 + k]);
-                    float amax = fmaxf(fmaxf(fabsf(hv[0]), fabsf(hv[1])), fmaxf(fabsf(hv[2]), fabsf(hv[3])));
-                    amax = lanes_reduce<8>(amax, OpMax());
-                    const float d = q8_1_scale(amax);
-                    int qv[4];
-                    q8_1_codes4(float4{hv[0], hv[1], hv[2], hv[3]}, amax, d, qv);
-                    const float qs = lanes_reduce<8>((float) (qv[0] + qv[1] + qv[2] + qv[3]), OpAddF());
-                    if (t0 + tok < nrows) {
-                        const int64_t hr = row0 + t0 + tok, col = (int64_t) (BM / 2) * bx + 4 * f4;
-                        *(uint32_t*) (H.q + hr * H.cols + col) = ((uint32_t) qv[0] & 0xFFu) |
-                                                                 ((uint32_t) qv[1] & 0xFFu) << 8 |
-                                                                 ((uint32_t) qv[2] & 0xFFu) << 16 |
-                                                                 ((uint32_t) qv[3] & 0xFFu) << 24;
-                        if ((f4 & 7) == 0) {
-                            H.d[hr * (H.cols / 32) + col / 32] = h2f(f2h(q8_1_finite(d)));
-                            H.m[hr * (H.cols / 32) + col / 32] = (int32_t) qs;
-                        }
+                    const int tok = 16 * tj + lr;
+                    if (tok < nrows) {
+                        const int64_t hi = (int64_t) (row0 + tok) * (H.cols / 32) + col / 32;
+                        const float qs = s_ex[NW * EX + wave * EX + 16 * tj + lr] + s_ex[NW * EX + (wave + 1) * EX + 16 * tj + lr];
+                        H.d[hi] = h2f(f2h(q8_1_finite(dd[tj])));
+                        H.m[hi] = (int32_t) qs;
                     }
                 }
-                __syncthreads();
             }
         } else {
             // out: weight row 16 t + 4 g + i of the wave, token 16 tj + lr
