@@ -194,6 +194,8 @@ __global__ void __launch_bounds__(kThreads) mmq_rows_kernel(const uint8_t* __res
 // the activation tile is double-buffered: one barrier per chunk) and Q8_0 (its wider raw rows fill the LDS)
 template <int T> constexpr int bn_of() { return T == TSX_Q8_0 || T == TSX_Q4_K ? 64 : 128; }
 constexpr int kChunk = 256;
+constexpr int kUpfrontTiles = 4;  // chunk loops with at most this many 16-token tiles decode kUpfrontUnits at a time
+constexpr int kUpfrontUnits = 2;
 constexpr int kBStride = kChunk + 8;  // fp16 per activation-tile row: 528 bytes puts 16 lanes' 16-byte reads on all banks
 constexpr int kMaxExpertsMmq = 512;
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -661,10 +663,10 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                 }
             };
             // unit u: every accumulator to the unit's scale (ROW: with the rows' ratios, rows 16 t + 4 g + i), then
-            // the unit's products added in place, token tile by token tile (each tile's activation fragment and
-            // ratio read just before its products); the next unit's weights are decoded while they run
-            v4i A[2];
-            auto step = [&](int u, auto row_c) {
+            // the unit's products (weight fragments Af) added in place, token tile by token tile (each tile's
+            // activation fragment and ratio read just before its products); NEXT: then the next unit's weights are
+            // decoded into Af while they run
+            auto step = [&](int u, v4i (&Af)[2], auto row_c, auto next_c) {
                 constexpr bool ROW = decltype(row_c)::value;
                 float rr[2][4];
                 if constexpr (ROW) {
@@ -693,24 +695,50 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                         v4f C;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) C[i] = acc[t][tj][i] * (ROW ? rh * rr[t][i] : rh);
-                        const v4f D = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, A[t]),
+                        const v4f D = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, Af[t]),
                                                                             __builtin_bit_cast(v8h, bf), C, 0, 0, 0);
 #pragma unroll
                         for (int i = 0; i < 4; ++i) acc[t][tj][i] = D[i];
                     }
                 }
                 __builtin_amdgcn_s_setprio(0);
-                if (u + 1 < 8) decode(u + 1, A);
+                if constexpr (decltype(next_c)::value) {
+                    if (u + 1 < 8) decode(u + 1, Af);
+                }
             };
-            decode(0, A);
-            step(0, std::integral_constant<bool, true>{});
-            // the next chunk's loads, issued behind the first unit's products rather than in a burst between
-            // barriers (the vector memory path takes ~0.7 us to accept a chunk's 72 KB)
-            if (c + 1 < nchunks) fetch(c + 1);
+            using No = std::integral_constant<bool, false>;
+            using Yes = std::integral_constant<bool, true>;
+            // (Q8_0's wider raw rows leave no registers for it, nor IQ3_S's fused launch beyond 2 tiles)
+            if constexpr (NTT <= (Q80 ? 0 : IQ3S && FUSE ? 2 : kUpfrontTiles)) {
+                // few token tiles: each unit's products are too short to cover its decode's chain of dependent
+                // LDS reads, so the units are decoded kUpfrontUnits at a time, their lookups in flight together (the
+                // registers are there: the kernel's allocation is set by the 8-tile path)
+                constexpr int UG = kUpfrontUnits;
+                v4i Au[UG][2];
+#pragma unroll
+                for (int h = 0; h < 8 / UG; ++h) {
+#pragma unroll
+                    for (int k = 0; k < UG; ++k) decode(UG * h + k, Au[k]);
+                    if (h == 0) {
+                        step(0, Au[0], Yes{}, No{});
+                        if (c + 1 < nchunks) fetch(c + 1);
+                    }
+#pragma unroll
+                    for (int k = h == 0 ? 1 : 0; k < UG; ++k)
+                        step(UG * h + k, Au[k], std::integral_constant<bool, Q80>{}, No{});
+                }
+            } else {
+                v4i A[2];
+                decode(0, A);
+                step(0, A, Yes{}, Yes{});
+                // the next chunk's loads, issued behind the first unit's products rather than in a burst between
+                // barriers (the vector memory path takes ~0.7 us to accept a chunk's 72 KB)
+                if (c + 1 < nchunks) fetch(c + 1);
 #pragma unroll 1
-            for (int u = 1; u < 8; ++u) {
-                if constexpr (Q80) step(u, std::integral_constant<bool, true>{});
-                else step(u, std::integral_constant<bool, false>{});
+                for (int u = 1; u < 8; ++u) {
+                    if constexpr (Q80) step(u, A, Yes{}, Yes{});
+                    else step(u, A, No{}, Yes{});
+                }
             }
             if constexpr (Q4K) {
                 // the chunk's min term in the chunk's last scale: sum over units u of -(dmin m / w')[row][u] *
@@ -791,8 +819,8 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                 const int tok = 16 * tj + lr;
                 if (tok < nrows)
                     *(uint32_t*) (H.q + (int64_t) (row0 + tok) * H.cols + col) =
-                        ((uint32_t) qv[0] & 0xFFu) | ((uint32_t) qv[1] & 0xFFu) << 8 | ((uint32_t) qv[2] & 0xFFu) << 16 |
-                        ((uint32_t) qv[3] & 0xFFu) << 24;
+                        ((uint32_t) qv[0] & 0xFFu) | ((uint32_t) qv[1] & 0xFFu) << 8 |
+                        ((uint32_t) qv[2] & 0xFFu) << 16 | ((uint32_t) qv[3] & 0xFFu) << 24;
             }
             __syncthreads();
             if ((wave & 1) == 0 && g == 0) {
@@ -801,7 +829,8 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                     const int tok = 16 * tj + lr;
                     if (tok < nrows) {
                         const int64_t hi = (int64_t) (row0 + tok) * (H.cols / 32) + col / 32;
-                        const float qs = s_ex[NW * EX + wave * EX + 16 * tj + lr] + s_ex[NW * EX + (wave + 1) * EX + 16 * tj + lr];
+                        const float* sq = s_ex + NW * EX + 16 * tj + lr;
+                        const float qs = sq[wave * EX] + sq[(wave + 1) * EX];
                         H.d[hi] = h2f(f2h(q8_1_finite(dd[tj])));
                         H.m[hi] = (int32_t) qs;
                     }
