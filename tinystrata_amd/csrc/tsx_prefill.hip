@@ -613,17 +613,46 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                 const int r = 16 * t + lr;
                 blk[t] = slab + r * RS + (int) ((roff(r) + (uint64_t) c * CB) & 15);
             }
-            // unit u's weight fragments (rows 16 t + lr, values 8 g .. 8 g + 7 of the unit)
-            auto decode = [&](int u, v4i (&A)[2]) {
+            // unit u's weight fragments (rows 16 t + lr, values 8 g .. 8 g + 7 of the unit), in two halves: raw()
+            // reads the unit's indices and scales (the slab and the per-unit arrays), expand() looks the codebooks up
+            // and forms the fp16 fragments, so that a unit's indices can be requested ahead of the products they
+            // would otherwise wait behind
+            struct Raw {
+                uint32_t a[2][3];
+            };
+            auto raw = [&](int u, Raw& R) {
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     const uint8_t* b = blk[t];
                     const int r = 16 * t + lr;
+                    if constexpr (T == TSX_IQ3_XXS) {
+                        const uint2 am = s_am[wave][u][r];
+                        R.a[t][0] = ld16(b + 2 + 8 * u + 2 * g);
+                        R.a[t][1] = am.x;  // aux word: scale and sign indices
+                        R.a[t][2] = am.y;  // the scale pair
+                    } else if constexpr (IQ3S) {
+                        R.a[t][0] = ld16(b + 2 + 8 * u + 2 * g) | ((uint32_t) b[66 + u] >> (2 * g)) << 16;
+                        R.a[t][1] = b[74 + 4 * u + g];
+                        R.a[t][2] = s_sc[wave][u][r];
+                    } else if constexpr (Q4K) {
+                        const uint8_t* q = b + 16 + 32 * (u >> 1) + 8 * g;
+                        R.a[t][0] = ld32a2(q);
+                        R.a[t][1] = ld32a2(q + 4);
+                        R.a[t][2] = s_sc[wave][u][r];
+                    } else {
+                        const uint8_t* q = b + 34 * u + 2 + 8 * g;
+                        R.a[t][0] = ld32a2(q);
+                        R.a[t][1] = ld32a2(q + 4);
+                        R.a[t][2] = s_sc[wave][u][r];
+                    }
+                }
+            };
+            auto expand = [&](int u, const Raw& R, v4i (&A)[2]) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
                     uint32_t f[4];
                     if constexpr (T == TSX_IQ3_XXS) {
-                        const uint32_t qp = ld16(b + 2 + 8 * u + 2 * g);
-                        const uint2 am = s_am[wave][u][r];
-                        const uint32_t aux = am.x, m = am.y;
+                        const uint32_t qp = R.a[t][0], aux = R.a[t][1], m = R.a[t][2];
                         const uint2 g0 = *(const uint2*) (s_tab + 2 * (qp & 255u));
                         const uint2 g1 = *(const uint2*) (s_tab + 2 * (qp >> 8));
                         const uint4 sm = *(const uint4*) (s_tab + GW + 4 * ((aux >> (7 * g)) & 127u));
@@ -632,40 +661,41 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                         f[2] = hmul(g1.x ^ sm.z, m);
                         f[3] = hmul(g1.y ^ sm.w, m);
                     } else if constexpr (IQ3S) {
-                        const uint32_t qp = ld16(b + 2 + 8 * u + 2 * g);
-                        const uint32_t qh = (uint32_t) b[66 + u] >> (2 * g);
+                        const uint32_t qp = R.a[t][0] & 0xFFFFu, qh = R.a[t][0] >> 16, m = R.a[t][2];
                         const uint32_t i0 = (qp & 255u) | (qh & 1u) << 8, i1 = (qp >> 8) | (qh & 2u) << 7;
                         const uint2 g0 = *(const uint2*) (s_tab + 2 * i0);
                         const uint2 g1 = *(const uint2*) (s_tab + 2 * i1);
-                        const uint4 sm = *(const uint4*) (s_tab + GW + 4 * (uint32_t) b[74 + 4 * u + g]);
-                        const uint32_t m = s_sc[wave][u][r];
+                        const uint4 sm = *(const uint4*) (s_tab + GW + 4 * R.a[t][1]);
                         f[0] = hmul(g0.x ^ sm.x, m);
                         f[1] = hmul(g0.y ^ sm.y, m);
                         f[2] = hmul(g1.x ^ sm.z, m);
                         f[3] = hmul(g1.y ^ sm.w, m);
                     } else if constexpr (Q4K) {
-                        const uint8_t* q = b + 16 + 32 * (u >> 1) + 8 * g;
                         const int sh = 4 * (u & 1);
-                        const uint32_t w0 = (ld32a2(q) >> sh) & 0x0F0F0F0Fu, w1 = (ld32a2(q + 4) >> sh) & 0x0F0F0F0Fu;
-                        const h2 sc = __builtin_bit_cast(h2, s_sc[wave][u][r]);
+                        const uint32_t w0 = (R.a[t][0] >> sh) & 0x0F0F0F0Fu, w1 = (R.a[t][1] >> sh) & 0x0F0F0F0Fu;
+                        const h2 sc = __builtin_bit_cast(h2, R.a[t][2]);
                         const h2 nsc = sc * (_Float16) -1024.0f;
                         nib_to_h(w0, sc, nsc, f[0], f[1]);
                         nib_to_h(w1, sc, nsc, f[2], f[3]);
                     } else {
-                        const uint8_t* q = b + 34 * u + 2 + 8 * g;
-                        const uint32_t m = s_sc[wave][u][r];
-                        i8_to_h(ld32a2(q), f[0], f[1]);
-                        i8_to_h(ld32a2(q + 4), f[2], f[3]);
+                        const uint32_t m = R.a[t][2];
+                        i8_to_h(R.a[t][0], f[0], f[1]);
+                        i8_to_h(R.a[t][1], f[2], f[3]);
 #pragma unroll
                         for (int k = 0; k < 4; ++k) f[k] = hmul(f[k], m);
                     }
                     A[t] = v4i{(int) f[0], (int) f[1], (int) f[2], (int) f[3]};
                 }
             };
+            auto decode = [&](int u, v4i (&A)[2]) {
+                Raw R;
+                raw(u, R);
+                expand(u, R, A);
+            };
             // unit u: every accumulator to the unit's scale (ROW: with the rows' ratios, rows 16 t + 4 g + i), then
             // the unit's products (weight fragments Af) added in place, token tile by token tile (each tile's
             // activation fragment and ratio read just before its products); NEXT: then the next unit's weights are
-            // decoded into Af while they run
+            // decoded into Af
             auto step = [&](int u, v4i (&Af)[2], auto row_c, auto next_c) {
                 constexpr bool ROW = decltype(row_c)::value;
                 float rr[2][4];
@@ -679,6 +709,12 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                         rr[t][2] = v.z;
                         rr[t][3] = v.w;
                     }
+                }
+                // NEXT (Q4_K, whose registers allow it): the next unit's raw words, requested ahead of this unit's
+                // products
+                Raw Rn;
+                if constexpr (decltype(next_c)::value && Q4K) {
+                    if (u + 1 < 8) raw(u + 1, Rn);
                 }
                 float4 rv[(NTT + 3) / 4];
 #pragma unroll
@@ -703,7 +739,11 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
                 }
                 __builtin_amdgcn_s_setprio(0);
                 if constexpr (decltype(next_c)::value) {
-                    if (u + 1 < 8) decode(u + 1, Af);
+                    if constexpr (Q4K) {
+                        if (u + 1 < 8) expand(u + 1, Rn, Af);
+                    } else {
+                        if (u + 1 < 8) decode(u + 1, Af);
+                    }
                 }
             };
             using No = std::integral_constant<bool, false>;
