@@ -419,7 +419,8 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1_kernel(LayerArgs a) {
     const float4* x4 = (const float4*) a.x;
     float4 xv[kXLoads];
 #pragma unroll
-    for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(max(xt, 0) + nxt * i, nq_all - 1)];
+    for (int i = 0; i < kXLoads; ++i)  // rounds past the row's end skipped (the same in every thread)
+        if (nxt * i < nq_all) xv[i] = x4[min(max(xt, 0) + nxt * i, nq_all - 1)];
     // the row loads below must not be issued ahead of these: a wait for these would then wait for the rows too
     __builtin_amdgcn_sched_barrier(0);
     const int rows_w = a.rows_w;
@@ -554,7 +555,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ LayerTables s_tab;
     __shared__ float s_part[kMaxEnt + kMaxTok][kRowsB];
-    __shared__ float s_sgate[kMaxTok];
+    __shared__ float s_sgate[kMaxTok];  // the token's shared-expert gate, sigmoid applied
 
     const int tid = threadIdx.x;
     const int T = a.n_tok, k = a.k, n_ent = T * k;
@@ -573,9 +574,11 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     // h: the Q8_1 planes (16-byte pieces; n_ff is a multiple of 128), or fp32 h (float4 quads) quantized here
     const int nh = a.h_fp32 ? P * FF / 4 : (P * FF + P * NUd * 4) / 16;
     const v4i* hsrc = (const v4i*) (a.h_fp32 ? (const void*) a.hf : (const void*) a.hc);
+    // (loads past the last piece are skipped: the condition is the same in every thread)
     v4i hv[kHLoads];
 #pragma unroll
-    for (int i = 0; i < kHLoads; ++i) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
+    for (int i = 0; i < kHLoads; ++i)
+        if (kThreadsB * i < nh) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
     const float sg = a.shared ? a.sgate[(int64_t) min(tid, T - 1) * a.sg_stride] : 0.f;
     const int ty = min(tid / kRowsB, T - 1), ry = tid % kRowsB;  // the y value this thread combines into
     const float y0 = a.y[(int64_t) ty * N + r0 + ry];
@@ -600,9 +603,11 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     auto issue = [&](int ch) {
         const int g0 = ch * gpc, np = min(gpc, G - g0) * ppg;
 #pragma unroll
-        for (int i = 0; i < kBLoads; ++i) {  // unconditional (clamped) loads keep the wait counts exact
-            const int q = min(tid + kThreadsB * i, np - 1), g = div_small(q, ppg, rppg), pp = q - g * ppg;
-            reg[i] = __builtin_nontemporal_load(gbl_at<v4i>((uintptr_t) gsrc(g0 + g)) + pp);
+        for (int i = 0; i < kBLoads; ++i) {  // rounds past the chunk's last piece are skipped (the same in every thread)
+            if (kThreadsB * i < np) {
+                const int q = min(tid + kThreadsB * i, np - 1), g = div_small(q, ppg, rppg), pp = q - g * ppg;
+                reg[i] = __builtin_nontemporal_load(gbl_at<v4i>((uintptr_t) gsrc(g0 + g)) + pp);
+            }
         }
     };
     issue(0);
@@ -610,7 +615,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     // h into LDS: the prefetched pieces, then any rest
-    if (tid < T) s_sgate[tid] = sg;
+    if (tid < T) s_sgate[tid] = 1.0f / (1.0f + expf(-sg));  // the shared expert's gate, ahead of the combine
     int8_t* s_hq = (int8_t*) (smem + a.slab_b + rep_lds_bytes<DT>());
     float* s_hd = (float*) (s_hq + (size_t) P * FF);
     if (a.h_fp32) {  // every Q8_1 block of h from its eight quads (consecutive lanes), as launch A would write it
@@ -667,13 +672,13 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
                 rr[m] = ri % kRowsB;
                 pos[m] = grp_lo(g0 + g);
                 v[m] = 0.f;
-                if (kThreadsB * m < items)  // the same in every thread (24-bit products: full-rate multiplies)
+                if (kThreadsB * m + (tid & ~63) < items)  // whole waves (24-bit products: full-rate multiplies)
                     unit_load<DT>((const uint8_t*) smem + __umul24(g, gb) + __umul24(rr[m], (uint32_t) d_row), u, w[m],
                                   grid);
             }
 #pragma unroll
             for (int m = 0; m < kItemsB1; ++m) {
-                if (kThreadsB * m < items) {
+                if (kThreadsB * m + (tid & ~63) < items) {
                     const int it = min(tid + kThreadsB * m, items - 1), u = it & (NUd - 1);
                     Act xa;
                     act_planes(s_hq + __umul24(pos[m], FF) + 32 * u, s_hd + (pos[m] << lgu) + u, xa);
@@ -683,7 +688,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
             }
 #pragma unroll
             for (int m = 0; m < kItemsB1; ++m) {
-                if (kThreadsB * m < items) {
+                if (kThreadsB * m + (tid & ~63) < items) {
                     const float t = NUd == 8 ? lanes_sum<8>(v[m]) : NUd == 16 ? lanes_sum<16>(v[m]) : lanes_sum<32>(v[m]);
                     if ((tid & (NUd - 1)) == 0 && tid + kThreadsB * m < items) s_part[pos[m]][rr[m]] = t;
                 }
@@ -738,8 +743,7 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
         float acc = wr[0] * s_part[ep[0]][r];
         for (int jj = 1; jj < k; ++jj) acc = __builtin_fmaf(wr[jj], s_part[ep[jj]][r], acc);
         if (a.shared) {
-            const float gs = 1.0f / (1.0f + expf(-s_sgate[t]));
-            acc += gs * s_part[n_ent + t][r];
+            acc += s_sgate[t] * s_part[n_ent + t][r];
         }
         a.y[(int64_t) t * N + r0 + r] = y0 + acc;
     }

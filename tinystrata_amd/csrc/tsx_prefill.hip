@@ -418,17 +418,17 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     };
     const int nu = w_cols / 32, nchunks = w_cols / kChunk;
     // the activation rows this thread loads (the same every chunk): rows past the tile's last take its last row
-    int64_t arow_b[BP];
+    int32_t arow_b[BP];  // row indices (32-bit: widened where the addresses are formed)
 #pragma unroll
     for (int h = 0; h < BP; ++h) {
         const int r = row0 + min((tid + NT * h) >> 4, nrows - 1);
-        arow_b[h] = xids ? (int64_t) xids[r] : (int64_t) r;
+        arow_b[h] = xids ? xids[r] : r;
     }
     // thread tid < kBN stages token tid's scales (tokens past the tile's last take its last row's)
-    int64_t arow_s;
+    int32_t arow_s;
     {
         const int r = row0 + min(tid, nrows - 1);
-        arow_s = xids ? (int64_t) xids[r] : (int64_t) r;
+        arow_s = xids ? xids[r] : r;
     }
 
     // chunk c in flight: this wave's raw weight pieces, the block's share of activation codes, and (threads below
@@ -447,14 +447,14 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
 #pragma unroll
         for (int h = 0; h < BP; ++h) {
             const int pi = tid + NT * h, q = pi & 15;
-            av[h] = *(const v4i*) (P.q + arow_b[h] * P.cols + kChunk * c + 16 * q);
+            av[h] = *(const v4i*) (P.q + (int64_t) arow_b[h] * P.cols + kChunk * c + 16 * q);
         }
         if (tid < kBN) {
-            const float4* dp = (const float4*) (P.d + arow_s * nu + 8 * c);
+            const float4* dp = (const float4*) (P.d + (int64_t) arow_s * nu + 8 * c);
             ad[0] = dp[0];
             ad[1] = dp[1];
             if constexpr (Q4K) {
-                const int4* mp = (const int4*) (P.m + arow_s * nu + 8 * c);
+                const int4* mp = (const int4*) (P.m + (int64_t) arow_s * nu + 8 * c);
                 am4[0] = mp[0];
                 am4[1] = mp[1];
             }
