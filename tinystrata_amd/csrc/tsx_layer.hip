@@ -419,8 +419,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1_kernel(LayerArgs a) {
     const float4* x4 = (const float4*) a.x;
     float4 xv[kXLoads];
 #pragma unroll
-    for (int i = 0; i < kXLoads; ++i)  // rounds past the row's end skipped (the same in every thread)
-        if (nxt * i < nq_all) xv[i] = x4[min(max(xt, 0) + nxt * i, nq_all - 1)];
+    for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(max(xt, 0) + nxt * i, nq_all - 1)];
     // the row loads below must not be issued ahead of these: a wait for these would then wait for the rows too
     __builtin_amdgcn_sched_barrier(0);
     const int rows_w = a.rows_w;
@@ -547,7 +546,9 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1_kernel(LayerArgs a) {
 // 8 rows of every used expert's down matrix (and the shared expert's: 8 contiguous rows each) into LDS with every
 // thread's loads in flight at once (chunks of groups when they exceed the slab), dots each row with its group's
 // entries (tpr lanes per row, as many rows at once as the block has lanes for) and combines in pick order.
-template <int DT>
+// NR: rounds of 16-byte row loads per thread in flight (kBLoads, or 1 when a chunk's pieces fit one round: fewer
+// redundant clamped loads, and waits that stay exact)
+template <int DT, int NR>
 __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
 #pragma clang fp contract(off)
     constexpr int RP = (rep_stores<DT>() + kThreadsB - 1) / kThreadsB;
@@ -574,11 +575,9 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     // h: the Q8_1 planes (16-byte pieces; n_ff is a multiple of 128), or fp32 h (float4 quads) quantized here
     const int nh = a.h_fp32 ? P * FF / 4 : (P * FF + P * NUd * 4) / 16;
     const v4i* hsrc = (const v4i*) (a.h_fp32 ? (const void*) a.hf : (const void*) a.hc);
-    // (loads past the last piece are skipped: the condition is the same in every thread)
     v4i hv[kHLoads];
 #pragma unroll
-    for (int i = 0; i < kHLoads; ++i)
-        if (kThreadsB * i < nh) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
+    for (int i = 0; i < kHLoads; ++i) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
     const float sg = a.shared ? a.sgate[(int64_t) min(tid, T - 1) * a.sg_stride] : 0.f;
     const int ty = min(tid / kRowsB, T - 1), ry = tid % kRowsB;  // the y value this thread combines into
     const float y0 = a.y[(int64_t) ty * N + r0 + ry];
@@ -599,15 +598,13 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     const int gb = (int) (kRowsB * d_row), ppg = gb / 16;  // bytes and 16-byte pieces of a group's 8 rows
     const int gpc = max(1, a.slab_b / gb), nchunks = (G + gpc - 1) / gpc;
     const float rppg = __builtin_amdgcn_rcpf((float) ppg);
-    v4i reg[kBLoads];
+    v4i reg[NR];
     auto issue = [&](int ch) {
         const int g0 = ch * gpc, np = min(gpc, G - g0) * ppg;
 #pragma unroll
-        for (int i = 0; i < kBLoads; ++i) {  // rounds past the chunk's last piece are skipped (the same in every thread)
-            if (kThreadsB * i < np) {
-                const int q = min(tid + kThreadsB * i, np - 1), g = div_small(q, ppg, rppg), pp = q - g * ppg;
-                reg[i] = __builtin_nontemporal_load(gbl_at<v4i>((uintptr_t) gsrc(g0 + g)) + pp);
-            }
+        for (int i = 0; i < NR; ++i) {  // unconditional (clamped) loads keep the wait counts exact
+            const int q = min(tid + kThreadsB * i, np - 1), g = div_small(q, ppg, rppg), pp = q - g * ppg;
+            reg[i] = __builtin_nontemporal_load(gbl_at<v4i>((uintptr_t) gsrc(g0 + g)) + pp);
         }
     };
     issue(0);
@@ -648,9 +645,9 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     for (int ch = 0; ch < nchunks; ++ch) {
         const int g0 = ch * gpc, gn = min(gpc, G - g0), np = gn * ppg;
 #pragma unroll
-        for (int i = 0; i < kBLoads; ++i)
+        for (int i = 0; i < NR; ++i)
             if (tid + kThreadsB * i < np) slab[tid + kThreadsB * i] = reg[i];
-        for (int q = tid + kThreadsB * kBLoads; q < np; q += kThreadsB) {  // a chunk larger than the loads in flight
+        for (int q = tid + kThreadsB * NR; q < np; q += kThreadsB) {  // a chunk larger than the loads in flight
             const int g = q / ppg, pp = q - g * ppg;
             slab[q] = gbl_at<v4i>((uintptr_t) gsrc(g0 + g))[pp];
         }
@@ -740,11 +737,22 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
         const int t = tid / kRowsB, r = tid % kRowsB;
         const float* wr = s_tab.wts + t * k;
         const int32_t* ep = s_tab.ent_pos + t * k;
-        float acc = wr[0] * s_part[ep[0]][r];
-        for (int jj = 1; jj < k; ++jj) acc = __builtin_fmaf(wr[jj], s_part[ep[jj]][r], acc);
-        if (a.shared) {
-            acc += s_sgate[t] * s_part[n_ent + t][r];
+        // eight picks at a time, their weight and part reads issued together (one LDS round trip per eight, not two
+        // per pick); the products are summed in pick order as before
+        float acc = 0.f;
+        for (int j0 = 0; j0 < k; j0 += 8) {
+            float wv[8], pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int jj = min(j0 + i, k - 1);
+                wv[i] = wr[jj];
+                pv[i] = s_part[ep[jj]][r];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (j0 + i < k) acc = j0 + i == 0 ? wv[i] * pv[i] : __builtin_fmaf(wv[i], pv[i], acc);
         }
+        if (a.shared) acc += s_sgate[t] * s_part[n_ent + t][r];
         a.y[(int64_t) t * N + r0 + r] = y0 + acc;
     }
 }
@@ -895,8 +903,9 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
         return 0;
     });
     with_type(L.d_type, [&](auto T) {
-        static const size_t limit = set_max_lds((const void*) layer_down_kernel<decltype(T)::value>);
-        lim_b = limit;
+        static const size_t limit = set_max_lds((const void*) layer_down_kernel<decltype(T)::value, kBLoads>);
+        static const size_t limit1 = set_max_lds((const void*) layer_down_kernel<decltype(T)::value, 1>);
+        lim_b = std::min(limit, limit1);
         return 0;
     });
     const size_t fixed_a = rep_bytes(L.gu_type) + x_planes_bytes(L, n_tok);
@@ -974,8 +983,11 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
             return launch_status("tsx_moe_decode_layer/gate-up");
         });
     if (rc != TSX_OK) return rc;
+    // one round of row loads when the largest chunk (the slab's groups, or every group the routing can make) fits it
+    const int gb = (int) (kRowsB * L.d_row), gmax = std::min(n_tok * k, n_expert) + (shared ? 1 : 0);
+    const bool one_round = (int64_t) std::min(std::max(1, slab_b / gb), gmax) * (gb / 16) <= kThreadsB;
     rc = with_type(L.d_type, [&](auto T) {
-        auto kern = layer_down_kernel<decltype(T)::value>;
+        auto kern = one_round ? layer_down_kernel<decltype(T)::value, 1> : layer_down_kernel<decltype(T)::value, kBLoads>;
         const size_t lds = (size_t) slab_b + fixed_b;
         kern<<<(unsigned) (L.n_embd / kRowsB), kThreadsB, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/down");
