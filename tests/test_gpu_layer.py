@@ -201,6 +201,29 @@ def test_decode_layer_residual_alias_and_replay():
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("k,ties", [(8, False), (8, True), (12, False), (12, True), (3, True)])
+def test_one_token_routing_matches_router(k, ties):
+    """At one token every launch A block routes the token itself, as far as its last pick (k 3 to 12): the layer's ids
+    and weights are the router kernel's bit for bit, also when probabilities tie (logits drawn from a few values, so
+    equal probabilities must go to the lower expert id)."""
+    gu, d, N, FF, E, _, shared, T = CONFIGS["c2_decode_iq3"]
+    L, p, order, W = make_layer(gu, d, N, FF, E, shared)
+    for seed in range(4):
+        rng = np.random.default_rng(100 + seed)
+        x = rng.normal(0, 1, (1, N)).astype(np.float32)
+        logits = (rng.integers(0, 6, (1, E)) * 0.5 if ties else rng.normal(0, 2, (1, E))).astype(np.float32)
+        sgate = rng.normal(0, 1, 1).astype(np.float32)
+        layer = moe.MoELayer(W, k, 1, torch.device("cuda"), fused=True)
+        y = torch.zeros((1, N), device="cuda")
+        layer(dev(x), dev(logits), dev(sgate), y)
+        ids_r = torch.empty((1, k), dtype=torch.int32, device="cuda")
+        wts_r = torch.empty((1, k), dtype=torch.float32, device="cuda")
+        ops.native_router_topk(dev(logits), k, ids_r, wts_r)
+        torch.cuda.synchronize()
+        assert (host(layer.ids) == host(ids_r)).all(), (seed, host(layer.ids), host(ids_r))
+        assert (host(layer.wts).view(np.uint32) == host(wts_r).view(np.uint32)).all(), seed
+
+
 def test_decode_layer_matches_kernel_by_kernel():
     """The two launches and the reference's kernel-by-kernel sequence route identically and agree to float order."""
     gu, d, N, FF, E, k, shared, T = CONFIGS["c3_verify_iq3"]

@@ -599,8 +599,10 @@ __device__ __forceinline__ void route_fetch(const float* __restrict__ l, int n_e
     for (int i = 0; i < kRouteV; ++i)  // unconditional (clamped) loads keep the wait counts exact
         v[i] = l[min(lane + 64 * i, n_expert - 1)];
 }
+// the softmax probabilities' order keys (NaN as -FLT_MAX) of the lane's V experts, sorted largest first with their
+// ids (a stable network: equal keys keep the lower id first)
 template <int V>
-__device__ __forceinline__ void route_select_v(const float (&lv)[kRouteV], int k, int lane, int32_t* ids, float* wts) {
+__device__ __forceinline__ void route_prep_v(const float (&lv)[kRouteV], int lane, uint32_t (&key)[V], uint32_t (&id)[V]) {
     float v[V];
     float mx = -INFINITY;
 #pragma unroll
@@ -616,16 +618,12 @@ __device__ __forceinline__ void route_select_v(const float (&lv)[kRouteV], int k
         sum += v[i];
     }
     const float rcp = 1.0f / reduce64(sum, OpAddF());
-    uint32_t key[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) {
         float p = v[i] * rcp;
         if (__builtin_isnan(p)) p = -FLT_MAX;
         key[i] = ord_key(p);
     }
-    // each lane's keys sorted largest first, with their ids (a stable network: equal keys keep the lower id first);
-    // a round's winner pops its head
-    uint32_t id[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) id[i] = (uint32_t) (64 * i + lane);
 #pragma unroll
@@ -639,6 +637,12 @@ __device__ __forceinline__ void route_select_v(const float (&lv)[kRouteV], int k
             id[j - 1] = sw ? i1 : i0;
             id[j] = sw ? i0 : i1;
         }
+}
+template <int V>
+__device__ __forceinline__ void route_select_v(const float (&lv)[kRouteV], int k, int lane, int32_t* ids, float* wts) {
+    // k rounds: the wave's largest head each, whose lane pops it
+    uint32_t key[V], id[V];
+    route_prep_v<V>(lv, lane, key, id);
     float sel_sum = 0.f, my_p = 0.f;
     int my_id = 0;
     for (int r = 0; r < k; ++r) {

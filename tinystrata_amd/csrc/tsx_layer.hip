@@ -61,7 +61,7 @@ constexpr int kNormRowThreads = 1024;  // the norm launch: threads per token row
 constexpr int kSlabB = 64 * 1024;     // most LDS bytes of a chunk of groups' down rows (8 rows of each)
 constexpr int kBLoads = kSlabB / 16 / kThreadsB;  // 16-byte loads per thread in flight: a whole chunk
 constexpr int kHLoads = 3;            // 16-byte pieces of h per thread prefetched by launch B
-constexpr int kItemsB1 = 2;           // launch B at one token: (row, unit) items per thread
+constexpr int kItemsB = 2;            // launch B: (row, unit) items per thread decoded together
 static_assert(kMaxTok <= kThreadsA / 64, "one wave per token in the routing");
 
 // the tables launch A leaves for launch B, at the start of the scratch buffer
@@ -654,40 +654,39 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
         __syncthreads();  // the chunk (and h, the codebooks) are in LDS
         if (ch + 1 < nchunks) issue(ch + 1);
         const int R = gn * kRowsB;
-        if (a.h_fp32 && (NUd == 8 || NUd == 16 || NUd == 32) && R * NUd <= kItemsB1 * kThreadsB) {
-            // one token: every group has one entry (position grp_lo).  The items (row, unit) go to consecutive
-            // threads, a row's NUd units to NUd lanes of one wave; a thread's items are decoded together (their
-            // codebook lookups in flight at once), then each row is reduced over its lanes with DPP
+        if (NUd == 8 || NUd == 16 || NUd == 32) {
+            // items (row, unit) to consecutive threads, a row's NUd units to NUd lanes of one wave (whose rows then
+            // share a group: NUd lanes per row, 64 / NUd rows per wave, 8 rows per group), in rounds of kThreadsB
+            // items, kItemsB at a time (their codebook lookups in flight together); each item's unit is dotted with
+            // every entry of its group and each row reduced over its lanes with DPP.  Rounds past the chunk's items
+            // are skipped by whole waves, so every thread has at most one item more than any other
             const int items = R * NUd, lgu = NUd == 8 ? 3 : NUd == 16 ? 4 : 5;
-            float v[kItemsB1];
-            int pos[kItemsB1], rr[kItemsB1];
-            Unit w[kItemsB1];
+            for (int m0 = 0; kThreadsB * m0 < items; m0 += kItemsB) {
+                int rr[kItemsB], lo[kItemsB], hi[kItemsB], uu[kItemsB];
+                Unit w[kItemsB];
 #pragma unroll
-            for (int m = 0; m < kItemsB1; ++m) {
-                const int it = min(tid + kThreadsB * m, items - 1), ri = it >> lgu, u = it & (NUd - 1);
-                const int g = ri / kRowsB;
-                rr[m] = ri % kRowsB;
-                pos[m] = grp_lo(g0 + g);
-                v[m] = 0.f;
-                if (kThreadsB * m + (tid & ~63) < items)  // whole waves (24-bit products: full-rate multiplies)
-                    unit_load<DT>((const uint8_t*) smem + __umul24(g, gb) + __umul24(rr[m], (uint32_t) d_row), u, w[m],
-                                  grid);
-            }
-#pragma unroll
-            for (int m = 0; m < kItemsB1; ++m) {
-                if (kThreadsB * m + (tid & ~63) < items) {
-                    const int it = min(tid + kThreadsB * m, items - 1), u = it & (NUd - 1);
-                    Act xa;
-                    act_planes(s_hq + __umul24(pos[m], FF) + 32 * u, s_hd + (pos[m] << lgu) + u, xa);
-                    int S, M;
-                    v[m] = unit_dot<DT>(w[m], xa, S, M);
+                for (int m = 0; m < kItemsB; ++m) {
+                    const int it = min(tid + kThreadsB * (m0 + m), items - 1), ri = it >> lgu, g = ri / kRowsB;
+                    rr[m] = ri % kRowsB;
+                    uu[m] = it & (NUd - 1);
+                    lo[m] = grp_lo(g0 + g);
+                    hi[m] = grp_hi(g0 + g);
+                    if (kThreadsB * (m0 + m) + (tid & ~63) < items)  // whole waves (24-bit products: full rate)
+                        unit_load<DT>((const uint8_t*) smem + __umul24(g, gb) + __umul24(rr[m], (uint32_t) d_row), uu[m],
+                                      w[m], grid);
                 }
-            }
 #pragma unroll
-            for (int m = 0; m < kItemsB1; ++m) {
-                if (kThreadsB * m + (tid & ~63) < items) {
-                    const float t = NUd == 8 ? lanes_sum<8>(v[m]) : NUd == 16 ? lanes_sum<16>(v[m]) : lanes_sum<32>(v[m]);
-                    if ((tid & (NUd - 1)) == 0 && tid + kThreadsB * m < items) s_part[pos[m]][rr[m]] = t;
+                for (int m = 0; m < kItemsB; ++m) {
+                    if (kThreadsB * (m0 + m) + (tid & ~63) < items) {
+                        for (int e = lo[m]; e < hi[m]; ++e) {  // the same in every lane of the wave
+                            Act xa;
+                            act_planes(s_hq + __umul24(e, FF) + 32 * uu[m], s_hd + (e << lgu) + uu[m], xa);
+                            int S, M;
+                            const float v = unit_dot<DT>(w[m], xa, S, M);
+                            const float t = NUd == 8 ? lanes_sum<8>(v) : NUd == 16 ? lanes_sum<16>(v) : lanes_sum<32>(v);
+                            if ((tid & (NUd - 1)) == 0 && tid + kThreadsB * (m0 + m) < items) s_part[e][rr[m]] = t;
+                        }
+                    }
                 }
             }
             __syncthreads();  // the chunk's rows are done before the next chunk overwrites the slab
