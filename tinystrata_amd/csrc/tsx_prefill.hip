@@ -273,7 +273,8 @@ template <int T, int NW, int NB> struct F16Layout {
     static constexpr int DL = RHO + lds_round(NB * 8 * 16 * RS * 4);
     static constexpr int DM = DL + lds_round(BN * 4);
     static constexpr int SCAN = DM + lds_round((Q4K ? NB * 8 * (BN + 16) : 1) * 4);
-    static constexpr int RAW = SCAN + lds_round((NW + 2) * 4);
+    static constexpr int DR = SCAN + lds_round((NW + 2) * 4);
+    static constexpr int RAW = DR + lds_round(BN * 4);
     static constexpr int TB = RAW + lds_round(NW * 32 * raw_stride<T>());
     static constexpr int BYTES = TB + NB * BN * kBStride * 2;
 };
@@ -370,6 +371,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
     int* const s_scan = reinterpret_cast<int*>(s_lds + L::SCAN);
     int& s_x = s_scan[NW];
     int& s_tile0 = s_scan[NW + 1];
+    int* const s_drow = reinterpret_cast<int*>(s_lds + L::DR);  // the output row of each token of the tile
     auto& s_raw = *reinterpret_cast<uint8_t(*)[NW][32 * RS]>(s_lds + L::RAW);
     auto& tB = *reinterpret_cast<_Float16(*)[NB][kBN * kBStride]>(s_lds + L::TB);
 
@@ -518,6 +520,9 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
         }
     }
     if (tid < kBN) s_dl[tid] = 1.0f;   // read back only by the same thread (stage)
+    // the tile's output rows, requested now rather than in the epilogue, where each token tile's row lookup would
+    // wait for its own round trip before that tile's stores (the block barriers before the epilogue order these)
+    if (!FUSE && tid < kBN) s_drow[tid] = ids ? ids[row0 + min(tid, nrows - 1)] : row0 + tid;
     if (lane < 32) s_dw[wave][lane] = 1.0f;  // read back only by the same wave (the row factors)
     fetch(0);
     if constexpr (TW > 0) {
@@ -882,7 +887,7 @@ __global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restr
             for (int tj = 0; tj < NTT; ++tj) {
                 const int tok = 16 * tj + lr;
                 if (tok < nrows) {
-                    const int64_t drow = ids ? ids[row0 + tok] : row0 + tok;
+                    const int64_t drow = s_drow[tok];
                     float* o = dst + drow * ld_dst + (int64_t) bx * BM + 32 * wave + 4 * g;
 #pragma unroll
                     for (int t = 0; t < 2; ++t)
