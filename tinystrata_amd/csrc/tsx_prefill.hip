@@ -190,9 +190,14 @@ __global__ void __launch_bounds__(kThreads) mmq_rows_kernel(const uint8_t* __res
 // activation codes are in flight in registers while the current one is multiplied, and the activation tile is
 // double-buffered when LDS allows (one block barrier per chunk).
 // sorted token rows per block tile: 128 for the codebook formats (the decode of a weight fragment serves more tokens,
-// and an expert's weights are read once per 128 of its rows); 64 for Q4_K (its experts are mostly small, and at 64
-// the activation tile is double-buffered: one barrier per chunk) and Q8_0 (its wider raw rows fill the LDS)
+// and an expert's weights are read once per 128 of its rows); 64 for Q4_K (its experts are mostly small) and Q8_0
+// (its wider raw rows fill the LDS)
 template <int T> constexpr int bn_of() { return T == TSX_Q8_0 || T == TSX_Q4_K ? 64 : 128; }
+// waves per block: 8 (256 weight rows), except Q4_K's 4 (128 rows) with one activation buffer, 69 KB of LDS, so that
+// two blocks share a CU.  A SIMD's two waves then come from different blocks: the older of two waves of one block
+// wins most issue slots and finishes a chunk ~1.5 us before the younger, which then runs alone until the chunk's
+// barrier, while waves of two blocks wait at different barriers (configs[3] 263 -> 258 us per layer)
+template <int T> constexpr int nw_of() { return T == TSX_Q4_K ? 4 : 8; }
 constexpr int kChunk = 256;
 constexpr int kUpfrontTiles = 4;  // chunk loops with at most this many 16-token tiles decode kUpfrontUnits at a time
 constexpr int kUpfrontUnits = 2;
@@ -278,7 +283,9 @@ template <int T, int NW, int NB> struct F16Layout {
     static constexpr int TB = RAW + lds_round(NW * 32 * raw_stride<T>());
     static constexpr int BYTES = TB + NB * BN * kBStride * 2;
 };
-template <int T, int NW> constexpr int f16_buffers() { return F16Layout<T, NW, 2>::BYTES <= 150 * 1024 ? 2 : 1; }
+template <int T, int NW> constexpr int f16_buffers() {
+    return T == TSX_Q4_K && NW == 4 ? 1 : F16Layout<T, NW, 2>::BYTES <= 150 * 1024 ? 2 : 1;
+}
 
 __device__ __forceinline__ uint32_t hmul(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * __builtin_bit_cast(h2, b));
@@ -334,12 +341,12 @@ __device__ __forceinline__ int block_scan(int v, int* s_wave, int& total) {
     return off + inc - v;
 }
 
-// FUSE: the gate/up product with SwiGLU and the Q8_1 of h fused in (NW = 8).  Block bx takes h columns
-// [128 bx, 128 bx + 128): wave w multiplies gate rows 128 bx + 16 w + [0, 16) (its first 16-row tile) and the up
-// rows n_ff further (its second), so that each lane holds matching gate and up outputs; the activation rows are
+// FUSE: the gate/up product with SwiGLU and the Q8_1 of h fused in (NW = nw_of<T>()).  Block bx takes h columns
+// [16 NW bx, 16 NW bx + 16 NW): wave w multiplies gate rows 16 NW bx + 16 w + [0, 16) (its first 16-row tile) and the
+// up rows n_ff further (its second), so that each lane holds matching gate and up outputs; the activation rows are
 // xids[sorted row] of P (sorted row r itself when xids is null); h leaves as Q8_1 planes H, one row per sorted row.
 template <int T, int NW, bool FUSE = false>
-__global__ void __launch_bounds__(64 * NW) mmq_f16_kernel(const uint8_t* __restrict__ w, uint64_t expert_bytes,
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) mmq_f16_kernel(const uint8_t* __restrict__ w, uint64_t expert_bytes,
                                                           uint64_t row_bytes, int w_cols, int n_exp, MmqPlanes P,
                                                           const int32_t* __restrict__ bounds,
                                                           const int32_t* __restrict__ ids, float* __restrict__ dst,
@@ -989,7 +996,7 @@ TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
     // the f16-MFMA tiles where the shape fits them (rows in multiples of 64), else the row-dot kernel
     if (p->w_cols % kChunk == 0 && p->w_rows % 64 == 0 && p->n <= kMaxExpertsMmq && aligned(p->w, 16) &&
         p->expert_bytes % 16 == 0) {
-        const int nw = p->w_rows % 256 == 0 ? 8 : p->w_rows % 128 == 0 ? 4 : 2;
+        const int nw = p->type == TSX_Q4_K && p->w_rows % 128 == 0 ? 4 : p->w_rows % 256 == 0 ? 8 : p->w_rows % 128 == 0 ? 4 : 2;
         return with_type(p->type, [&](auto T) {
             constexpr int TT = decltype(T)::value;
             const int64_t max_tiles = (p->total_rows + bn_of<TT>() - 1) / bn_of<TT>() + p->n;
@@ -1041,8 +1048,9 @@ TSX_API int tsx_moe_mmq_gate_up_swiglu(const void* w, int type, int64_t n_ff, in
     return with_type(type, [&](auto T) {
         constexpr int BN = bn_of<decltype(T)::value>();
         const int64_t max_tiles = (n_rows + BN - 1) / BN + n_exp;
-        const dim3 grid((unsigned) (n_ff / 128), (unsigned) max_tiles);
-        mmq_f16_kernel<decltype(T)::value, 8, true><<<grid, 512, 0, s>>>(
+        constexpr int NW = nw_of<decltype(T)::value>();
+        const dim3 grid((unsigned) (n_ff / (16 * NW)), (unsigned) max_tiles);
+        mmq_f16_kernel<decltype(T)::value, NW, true><<<grid, 64 * NW, 0, s>>>(
             (const uint8_t*) w, expert_bytes, rb, (int) n_embd, n_exp, P, bounds, nullptr, nullptr, 0, xids, H, (int) n_ff);
         return launch_status("tsx_moe_mmq_gate_up_swiglu");
     });
