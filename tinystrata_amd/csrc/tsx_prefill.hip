@@ -201,6 +201,9 @@ template <int T> constexpr int nw_of() { return T == TSX_Q4_K ? 4 : 8; }
 constexpr int kChunk = 256;
 constexpr int kUpfrontTiles = 4;  // chunk loops with at most this many 16-token tiles decode kUpfrontUnits at a time
 constexpr int kUpfrontUnits = 2;
+// products of at most this many columns (a down product) take two 256-row column blocks per block in turn: the
+// second's first chunk is requested during the first's last, hiding a block's set-up and first-chunk latency
+constexpr int kPassCols = 512;
 constexpr int kBStride = kChunk + 8;  // fp16 per activation-tile row: 528 bytes puts 16 lanes' 16-byte reads on all banks
 constexpr int kMaxExpertsMmq = 512;
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -345,7 +348,7 @@ __device__ __forceinline__ int block_scan(int v, int* s_wave, int& total) {
 // [16 NW bx, 16 NW bx + 16 NW): wave w multiplies gate rows 16 NW bx + 16 w + [0, 16) (its first 16-row tile) and the
 // up rows n_ff further (its second), so that each lane holds matching gate and up outputs; the activation rows are
 // xids[sorted row] of P (sorted row r itself when xids is null); h leaves as Q8_1 planes H, one row per sorted row.
-template <int T, int NW, bool FUSE = false>
+template <int T, int NW, bool FUSE = false, int CP = 1>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) mmq_f16_kernel(const uint8_t* __restrict__ w, uint64_t expert_bytes,
                                                           uint64_t row_bytes, int w_cols, int n_exp, MmqPlanes P,
                                                           const int32_t* __restrict__ bounds,
@@ -419,7 +422,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     const int row0 = bounds[x] + s_tile0 * kBN;
     const int nrows = min(kBN, bounds[x + 1] - row0);
     const int ntt = (nrows + 15) >> 4;  // 16-token MFMA tiles with rows in them
-    const int wrow = FUSE ? (BM / 2) * bx + 16 * wave : bx * BM + 32 * wave;
+    const int wrow = FUSE ? (BM / 2) * bx + 16 * wave : bx * CP * BM + 32 * wave;
     const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) wrow * row_bytes;
     // byte offset of the wave's row r (0-31) from wbase: FUSE rows 16-31 are the up rows of rows 0-15
     auto roff = [&](int r) -> uint64_t {
@@ -445,13 +448,15 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     v4i rw[RW], av[BP];
     float4 ad[2];
     int4 am4[2];
-    auto fetch = [&](int c) {
+    auto fetch = [&](int v) {
+        const int pass = CP > 1 ? v / nchunks : 0, c = v - pass * nchunks;
+        const uint8_t* wb = wbase + (uint64_t) pass * BM * row_bytes;  // BM rows further per column pass
 #pragma unroll
         for (int i = 0; i < RW; ++i) {
             const int q = min(lane + 64 * i, 32 * PR - 1), r = q / PR, pc = q - r * PR;
             const uint64_t o = roff(r) + (uint64_t) c * CB;
             const int need = (int) (((o & 15) + CB + 15) / 16);  // pieces that start before the block's end
-            rw[i] = __builtin_nontemporal_load((const v4i*) (wbase + (o & ~(uint64_t) 15)) + min(pc, need - 1));
+            rw[i] = __builtin_nontemporal_load((const v4i*) (wb + (o & ~(uint64_t) 15)) + min(pc, need - 1));
         }
 #pragma unroll
         for (int h = 0; h < BP; ++h) {
@@ -551,8 +556,38 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[t][tj][i] = 0.f;
 
-        for (int c = 0; c < nchunks; ++c) {
-            const int buf = NB == 2 ? (c & 1) : 0;
+        // to the outputs' scale: the row's last w' and the token's last D'
+        auto to_scale = [&]() __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float4 w4 = *(const float4*) &s_dw[wave][16 * t + 4 * g];
+                const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int tj = 0; tj < NTT; ++tj) {
+                    const float dl = s_dl[16 * tj + lr];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[t][tj][i] = acc[t][tj][i] * wv[i] * dl;
+                }
+            }
+        };
+        // out: weight row 16 t + 4 g + i of the wave (column pass pass), token 16 tj + lr
+        auto out_rows = [&](int pass) __attribute__((always_inline)) {
+#pragma unroll
+            for (int tj = 0; tj < NTT; ++tj) {
+                const int tok = 16 * tj + lr;
+                if (tok < nrows) {
+                    const int64_t drow = s_drow[tok];
+                    float* o = dst + drow * ld_dst + (int64_t) (bx * CP + pass) * BM + 32 * wave + 4 * g;
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) o[16 * t + i] = acc[t][tj][i];
+                }
+            }
+        };
+        for (int v = 0; v < CP * nchunks; ++v) {
+            const int pass = CP > 1 ? v / nchunks : 0, c = v - pass * nchunks;
+            const int buf = NB == 2 ? (v & 1) : 0;
             const _Float16* B = tB[buf];
             const uint8_t* slab = s_raw[wave];
             const lds_ptr<const v4i> bq = lds_base<v4i>(B + lr * kBStride + 8 * g);  // this lane's activation pieces
@@ -773,7 +808,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                     for (int k = 0; k < UG; ++k) decode(UG * h + k, Au[k]);
                     if (h == 0) {
                         step(0, Au[0], Yes{}, No{});
-                        if (c + 1 < nchunks) fetch(c + 1);
+                        if (v + 1 < CP * nchunks) fetch(v + 1);
                     }
 #pragma unroll
                     for (int k = h == 0 ? 1 : 0; k < UG; ++k)
@@ -785,7 +820,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                 step(0, A, Yes{}, Yes{});
                 // the next chunk's loads, issued behind the first unit's products rather than in a burst between
                 // barriers (the vector memory path takes ~0.7 us to accept a chunk's 72 KB)
-                if (c + 1 < nchunks) fetch(c + 1);
+                if (v + 1 < CP * nchunks) fetch(v + 1);
 #pragma unroll 1
                 for (int u = 1; u < 8; ++u) {
                     if constexpr (Q80) step(u, A, Yes{}, Yes{});
@@ -814,26 +849,27 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                     }
                 }
             }
-            if (c + 1 < nchunks) {
-                if constexpr (NB == 1) __syncthreads();  // every wave is done with the single activation tile
+            if constexpr (CP > 1) {
+                if (c == nchunks - 1) {  // the pass's outputs, then the next pass's rows from zero
+                    to_scale();
+                    out_rows(pass);
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+#pragma unroll
+                        for (int tj = 0; tj < NTT; ++tj)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) acc[t][tj][i] = 0.f;
+                }
+            }
+            if (v + 1 < CP * nchunks) {
+                // every wave is done with the single activation tile (and, after a pass, with the tokens' D')
+                if (NB == 1 || (CP > 1 && c == nchunks - 1)) __syncthreads();
                 wave_lds_order();                        // this wave is done with its raw slab and factor rows
-                stage(NB == 2 ? (c + 1) & 1 : 0);
+                stage(NB == 2 ? (v + 1) & 1 : 0);
                 __syncthreads();
             }
         }
-        // to the outputs' scale: the row's last w' and the token's last D'
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const float4 w4 = *(const float4*) &s_dw[wave][16 * t + 4 * g];
-            const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-            for (int tj = 0; tj < NTT; ++tj) {
-                const float dl = s_dl[16 * tj + lr];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][tj][i] = acc[t][tj][i] * wv[i] * dl;
-            }
-        }
-
+        if constexpr (CP == 1) to_scale();
         if constexpr (FUSE) {
 #pragma clang fp contract(off)
             // h = silu(gate) * up in registers (lane: h columns 16 w + 4 g + i, tokens 16 tj + lr), the product
@@ -888,20 +924,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                     }
                 }
             }
-        } else {
-            // out: weight row 16 t + 4 g + i of the wave, token 16 tj + lr
-#pragma unroll
-            for (int tj = 0; tj < NTT; ++tj) {
-                const int tok = 16 * tj + lr;
-                if (tok < nrows) {
-                    const int64_t drow = s_drow[tok];
-                    float* o = dst + drow * ld_dst + (int64_t) bx * BM + 32 * wave + 4 * g;
-#pragma unroll
-                    for (int t = 0; t < 2; ++t)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) o[16 * t + i] = acc[t][tj][i];
-                }
-            }
+        } else if constexpr (CP == 1) {
+            out_rows(0);
         }
     };
     // partial tiles run the next size up in {1, 2, 3, 4, 6, 8} 16-token tiles (the extra ones multiply padding)
@@ -1002,7 +1026,10 @@ TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
             const int64_t max_tiles = (p->total_rows + bn_of<TT>() - 1) / bn_of<TT>() + p->n;
             const dim3 grid((unsigned) (p->w_rows / (32 * nw)), (unsigned) max_tiles);
             const uint8_t* w = (const uint8_t*) p->w;
-            if (nw == 8)
+            if (nw == 8 && p->w_cols <= kPassCols && p->w_rows % 512 == 0)
+                mmq_f16_kernel<TT, 8, false, 2><<<dim3(grid.x / 2, grid.y), 512, 0, s>>>(
+                    w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds, p->ids, p->dst, p->ld_dst);
+            else if (nw == 8)
                 mmq_f16_kernel<TT, 8><<<grid, 512, 0, s>>>(w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds,
                                                            p->ids, p->dst, p->ld_dst);
             else if (nw == 4)
