@@ -171,12 +171,7 @@ class MoELayer:
     def _prefill(self, x, logits, sgate, y):
         W, L, k, N, FF = self.W, self.W.L, self.k, self.N, self.FF
         if self.fused_prefill:
-            # the tokens' Q8_1 and the shared expert's products first: they need no routing, so the shared
-            # expert's blocks run while the router and the sort (a few dozen blocks) leave the CUs idle
-            self._prefill_shared(x)
-            ops.native_router_topk(logits, k, self.ids, self.wts)
-            bounds, ed, et, rinv, mr = ops.route_sort(self.ids, k, W.n_expert, bufs=self.sort)
-            self._prefill_fused(x, sgate, y, bounds, et, rinv)
+            self._prefill_fused(x, logits, sgate, y)
             return
         ops.native_router_topk(logits, k, self.ids, self.wts)
         bounds, ed, et, rinv, mr = ops.route_sort(self.ids, k, W.n_expert, bufs=self.sort)
@@ -197,29 +192,33 @@ class MoELayer:
             ops.mmq_run(sh[L.down_off:], L.d_type, N, FF, W.stride, 1, self.shq, self.sh_bounds, None, T, self.sh, N)
         self._combine(y, sgate, prow=rinv)
 
-    def _prefill_shared(self, x):
-        W, L, N, FF, T = self.W, self.W.L, self.N, self.FF, self.n_tok
+    def _prefill_fused(self, x, logits, sgate, y):
+        W, L, k, N, FF, T = self.W, self.W.L, self.k, self.N, self.FF, self.n_tok
+        main = torch.cuda.current_stream()
         ops.mmq_quantize(x, None, L.gu_type, N, N, T, xq=self.txq)  # every token once; routed rows read it via et
         if W.shared is not None:
-            # the shared expert's two products on a second stream, alongside the routing and the routed products:
-            # its 4 x ceil(T / 128) blocks fill the CUs those launches leave idle
             if self.side is None:
                 self.side = torch.cuda.Stream(device=x.device)
-            self.side.wait_stream(torch.cuda.current_stream())
+                self.x_ready = torch.cuda.Event()
+            self.x_ready.record(main)
+        ops.native_router_topk(logits, k, self.ids, self.wts)
+        bounds, ed, et, rinv, mr = ops.route_sort(self.ids, k, W.n_expert, bufs=self.sort)
+        ops.mmq_gate_up_swiglu(W.blobs, L.gu_type, FF, N, W.stride, W.n_expert, self.txq, T, et, bounds, self.n_ent,
+                               hq=self.mhq)
+        ops.mmq_run(W.blobs[L.down_off:], L.d_type, N, FF, W.stride, W.n_expert, self.mhq, bounds, None, self.n_ent,
+                    self.parts, N)
+        if W.shared is not None:
+            # the shared expert's two products on a second stream: they need only the tokens' Q8_1, so they run
+            # beside the router, the sort and the routed products, filling the CUs those launches leave idle.  They
+            # are issued after the routed chain so that a captured graph keeps that chain and the combine on one queue
+            # (a wait across queues left 6-10 us gaps on the critical path); the shared chain ends long before the
+            # combine waits for it
+            self.side.wait_event(self.x_ready)
             with torch.cuda.stream(self.side):
                 sh = W.shared
                 ops.mmq_gate_up_swiglu(sh, L.gu_type, FF, N, W.stride, 1, self.txq, T, None, self.sh_bounds, T,
                                        hq=self.shq)
                 ops.mmq_run(sh[L.down_off:], L.d_type, N, FF, W.stride, 1, self.shq, self.sh_bounds, None, T, self.sh,
                             N)
-
-    def _prefill_fused(self, x, sgate, y, bounds, et, rinv):
-        W, L, k, N, FF, T = self.W, self.W.L, self.k, self.N, self.FF, self.n_tok
-        main = torch.cuda.current_stream()
-        ops.mmq_gate_up_swiglu(W.blobs, L.gu_type, FF, N, W.stride, W.n_expert, self.txq, T, et, bounds, self.n_ent,
-                               hq=self.mhq)
-        ops.mmq_run(W.blobs[L.down_off:], L.d_type, N, FF, W.stride, W.n_expert, self.mhq, bounds, None, self.n_ent,
-                    self.parts, N)
-        if W.shared is not None:
             main.wait_stream(self.side)
         self._combine(y, sgate, prow=rinv)
