@@ -321,15 +321,15 @@ def test_expert_grouped_grid_groups_invariant():
 
 # ------------------------------------------------------------------ grouped prompt products
 @pytest.mark.parametrize("t", TYPES)
-@pytest.mark.parametrize("w_cols", [512, 2048])
+@pytest.mark.parametrize("w_cols", [256, 512, 2048])
 @pytest.mark.parametrize("w_rows", [64, 128, 256, 512, 96])
 def test_mmq_run_skewed_groups(t, w_cols, w_rows):
     """One grouped product over experts with 0, 1, 17, 70, 130, 255, 256 and 530 rows (tile tails, empty experts,
     several tiles, whole tiles, an expert over 500 rows as configs[4]'s Zipf routing makes),
     rows scattered to dst through ids; against the oracle's per-row dot on the same Q8_1 codes.  64, 128 and 256
     weight rows take the MFMA tiles with 2, 4 and 8 waves (Q4_K: 4 waves for 128 and 256, two blocks per CU; 512 IQ3
-    columns: rows that start off 16-byte alignment); 512 rows of 512 columns take two 256-row column blocks per block
-    in turn (every type but Q4_K); 96 rows the row-dot kernel."""
+    columns: rows that start off 16-byte alignment); 512 rows of at most 512 columns take two 256-row column blocks per
+    block in turn (every type but Q4_K; 256 columns: one chunk per pass); 96 rows the row-dot kernel."""
     rng = np.random.default_rng(t + w_cols + w_rows)
     counts = [0, 70, 1, 130, 17, 530, 255, 256]
     n, total = len(counts), sum(counts)
