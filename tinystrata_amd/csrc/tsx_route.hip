@@ -135,29 +135,33 @@ __global__ void __launch_bounds__(kSortThreads) route_sort_kernel(const int32_t*
     __shared__ int s_wsum[kSortWaves], s_wmax[kSortWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile0 = blockIdx.x * kSortThreads;
-    for (int i = tid; i < kSortWaves * n_expert; i += kSortThreads) wcnt[i / n_expert][i % n_expert] =
-        wbef[i / n_expert][i % n_expert] = 0;
+    for (int i = tid; i < kSortWaves * n_expert; i += kSortThreads) wcnt[i / n_expert][i % n_expert] = 0;
     __syncthreads();
-    // every entry's expert counted (a wave's 64 entries lie in one tile), kSortBatch tiles' ids requested at once so
-    // that one load latency covers them
-    for (int base = 0; base < n_ent; base += kSortThreads * kSortBatch) {
-        int xs[kSortBatch];
+    // every entry's expert counted (a wave's 64 entries lie in one tile) in entries [lo, hi), kSortBatch tiles' ids
+    // requested at once so that one load latency covers them
+    auto count = [&](int lo, int hi) {
+        for (int base = lo; base < hi; base += kSortThreads * kSortBatch) {
+            int xs[kSortBatch];
 #pragma unroll
-        for (int j = 0; j < kSortBatch; ++j) {
-            const int e = base + j * kSortThreads + tid;
-            xs[j] = e < n_ent ? ids[e] : -1;
-        }
+            for (int j = 0; j < kSortBatch; ++j) {
+                const int e = base + j * kSortThreads + tid;
+                xs[j] = e < hi ? ids[e] : -1;
+            }
 #pragma unroll
-        for (int j = 0; j < kSortBatch; ++j) {
-            const int x = xs[j];
-            if (x >= 0 && x < n_expert) {  // an id out of range is dropped
+            for (int j = 0; j < kSortBatch; ++j) {
+                const int x = xs[j];
                 // LDS atomics into the wave's own counts: no other wave touches them, and a wave's lanes share an
-                // expert a few times at most (a token picks an expert once)
-                atomicAdd(&wcnt[wave][x], 1);
-                if (base + j * kSortThreads < tile0) atomicAdd(&wbef[wave][x], 1);
+                // expert a few times at most (a token picks an expert once); an id out of range is dropped
+                if (x >= 0 && x < n_expert) atomicAdd(&wcnt[wave][x], 1);
             }
         }
-    }
+    };
+    // the earlier tiles first: the wave's counts then are its counts before this block's tile (copied by the wave
+    // itself, after its own atomics), and the rest of the entries complete them
+    count(0, min(tile0, n_ent));
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    for (int xx = lane; xx < n_expert; xx += 64) wbef[wave][xx] = wcnt[wave][xx];
+    count(min(tile0, n_ent), n_ent);
     __syncthreads();
     for (int xx = tid; xx < n_expert; xx += kSortThreads) {  // the waves' counts summed (wcnt cleared for the scatter)
         int c = 0, b = 0;
