@@ -221,6 +221,14 @@ TSX_API size_t tsx_moe_mmq_q8_bytes(int64_t rows, int64_t cols);
  * Replaces strata::prefill::mmq::quantize (include/strata/prefill/moe_mmq.hpp:39-41; src/prefill/moe_mmq.cu:309-325). */
 TSX_API int tsx_moe_mmq_quantize(const float* x, const int32_t* ids, void* xq, int type, int64_t cols, int64_t ld,
                                  int64_t rows, void* stream);
+/* tsx_moe_mmq_quantize of the `rows` token rows of x (ids = NULL) and tsx_moe_router_topk of their logits
+ * ([rows][n_expert]) in one launch: the two are independent, so their blocks share it.  The same bytes as the two
+ * calls; x 16-byte aligned with ld a multiple of 4, n_expert and k as tsx_moe_router_topk.  Replaces the pair
+ * native_router_topk (include/strata/kernels/native_router.hpp:5-6) + mmq::quantize of the tokens
+ * (include/strata/prefill/moe_mmq.hpp:39-41) at the prompt call site (src/qwen35/q36_engine.cu:2855-2872). */
+TSX_API int tsx_moe_mmq_quantize_route(const float* x, void* xq, int type, int64_t cols, int64_t ld, int64_t rows,
+                                       const float* logits, int32_t* ids, float* weights, int n_expert, int k,
+                                       void* stream);
 /* One grouped product over n experts whose weights lie expert_bytes apart from w: for expert x, activation rows
  * [bounds[x], bounds[x+1]) of xq times its [w_rows][w_cols] matrix into dst rows ids[row] (row when ids is null),
  * ld_dst floats apart.  bounds on the device (n + 1 ints); total_rows = rows of xq.  max_rows may be 0: the tiles

@@ -208,6 +208,31 @@ def test_mmq_quantize_planes_exact(pad, rows):
     assert (q[rows:] == 0).all() and (d[rows:] == 0).all() and (m[rows:] == 0).all()
 
 
+@pytest.mark.parametrize("rows,E,k", [(1, 64, 8), (37, 128, 8), (300, 256, 8), (513, 512, 16)])
+def test_mmq_quantize_route_matches_the_two_calls(rows, E, k):
+    """tsx_moe_mmq_quantize_route: the token planes byte for byte as tsx_moe_mmq_quantize (every row, the padding
+    rows zeroed over garbage), and ids / weights bit for bit as tsx_moe_router_topk, with tied logits in some rows."""
+    rng = np.random.default_rng(rows + E + k)
+    cols = 512
+    x = rng.normal(0, 1, (rows, cols)).astype(np.float32)
+    if rows > 3:
+        x[3, 32:64] = 0.0                            # an all-zero block
+    logits = rng.normal(0, 1, (rows, E)).astype(np.float32)
+    if rows > 5:
+        logits[5, :] = 0.25                          # every expert tied
+        logits[4, 7:19] = logits[4, 6]               # ties around a pick
+    xd, ld = dev(x), dev(logits)
+    sep = host(ops.mmq_quantize(xd, None, IQ3_XXS, cols, cols, rows))
+    ids_s = torch.empty((rows, k), dtype=torch.int32, device="cuda")
+    wts_s = torch.empty((rows, k), dtype=torch.float32, device="cuda")
+    ops.native_router_topk(ld, k, ids_s, wts_s)
+    xq0 = torch.full((ops.mmq_q8_bytes(rows, cols),), 0xAB, dtype=torch.uint8, device="cuda")
+    xq, ids, wts = ops.mmq_quantize_route(xd, IQ3_XXS, ld, k, xq=xq0)
+    assert (host(xq) == sep).all()
+    assert (host(ids) == host(ids_s)).all()
+    assert (host(wts).view(np.int32) == host(wts_s).view(np.int32)).all()
+
+
 @pytest.mark.parametrize("shared,prow,n", [(False, False, 2048), (True, True, 2048), (True, False, 4096),
                                            (False, True, 96)])
 def test_combine_norm(shared, prow, n):

@@ -181,6 +181,7 @@ SIGNATURES = {
     "tsx_moe_combine_norm": (I32, [P, P, P, P, I32, P, P, I32, I32, I32, P, C.c_float, P, P, P]),
     "tsx_moe_mmq_q8_bytes": (SZ, [I64, I64]),
     "tsx_moe_mmq_quantize": (I32, [P, P, P, I32, I64, I64, I64, P]),
+    "tsx_moe_mmq_quantize_route": (I32, [P, P, I32, I64, I64, I64, P, P, P, I32, I32, P]),
     "tsx_moe_mmq_run": (I32, [C.POINTER(MmqProduct), P]),
     "tsx_moe_mmq_swiglu": (I32, [P, P, I64, I64, I32, P]),
     "tsx_moe_mmq_gate_up_swiglu": (I32, [P, I32, I64, I64, U64, I32, P, I64, P, P, I64, P, P]),

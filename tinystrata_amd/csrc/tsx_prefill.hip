@@ -57,15 +57,10 @@ __device__ __forceinline__ void zero_pad_rows(const MmqPlanes& P, int64_t rows, 
 // 8 lanes per Q8_1 block, 4 values each (float4 loads, 4-byte code stores, DPP reductions within the 8 lanes):
 // row i of the output is row ids[i] (or i) of x.  The codes of q8_1_store32, byte for byte.  Blocks past the
 // quantize's own zero the padding rows.
-__global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __restrict__ x, const int32_t* __restrict__ ids,
-                                                                MmqPlanes P, int64_t cols, int64_t ld, int64_t rows,
-                                                                int qblocks) {
-    if ((int) blockIdx.x >= qblocks) {
-        zero_pad_rows(P, rows, (int) blockIdx.x - qblocks);
-        return;
-    }
+__device__ __forceinline__ void quantize_quads(const float* __restrict__ x, const int32_t* __restrict__ ids,
+                                               const MmqPlanes& P, int64_t cols, int64_t ld, int64_t rows, int block) {
     const int64_t nq = cols / 4;  // quads per row
-    const int64_t qi = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t qi = (int64_t) block * blockDim.x + threadIdx.x;
     const bool valid = qi < rows * nq;
     const int64_t qc = valid ? qi : rows * nq - 1;  // every lane takes part in the reductions
     const int64_t i = qc / nq, c4 = qc % nq;
@@ -86,6 +81,32 @@ __global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __r
             P.d[i * (cols / 32) + b] = h2f(f2h(q8_1_finite(d)));
             P.m[i * (cols / 32) + b] = (int32_t) qs;
         }
+    }
+}
+__global__ void __launch_bounds__(kThreads) mmq_quantize_kernel(const float* __restrict__ x, const int32_t* __restrict__ ids,
+                                                                MmqPlanes P, int64_t cols, int64_t ld, int64_t rows,
+                                                                int qblocks) {
+    if ((int) blockIdx.x >= qblocks) zero_pad_rows(P, rows, (int) blockIdx.x - qblocks);
+    else quantize_quads(x, ids, P, cols, ld, rows, (int) blockIdx.x);
+}
+// the prompt's token quantize and its router top-k in one launch (independent work): the first rblocks route four
+// tokens each (a wave per token, route_token; their dependent loads start first), the next qblocks quantize and the
+// last kPadBlocks zero the padding rows
+__global__ void __launch_bounds__(kThreads) mmq_quantize_route_kernel(const float* __restrict__ x, MmqPlanes P,
+                                                                      int64_t cols, int64_t ld, int64_t rows, int qblocks,
+                                                                      int rblocks, const float* __restrict__ logits,
+                                                                      int32_t* __restrict__ rids, float* __restrict__ rwts,
+                                                                      int n_expert, int k) {
+    const int b = (int) blockIdx.x;
+    if (b < rblocks) {
+        const int t = b * 4 + (int) (threadIdx.x >> 6);
+        if (t < rows)
+            route_token(logits + (int64_t) t * n_expert, n_expert, k, (int) (threadIdx.x & 63), rids + (int64_t) t * k,
+                        rwts + (int64_t) t * k);
+    } else if (b < rblocks + qblocks) {
+        quantize_quads(x, nullptr, P, cols, ld, rows, b - rblocks);
+    } else {
+        zero_pad_rows(P, rows, b - rblocks - qblocks);
     }
 }
 
@@ -1002,6 +1023,28 @@ TSX_API int tsx_moe_mmq_quantize(const float* x, const int32_t* ids, void* xq, i
         mmq_quantize1_kernel<<<(unsigned) (qb + kPadBlocks), kThreads, 0, s>>>(x, ids, P, cols, ld, rows, qb);
     }
     return launch_status("tsx_moe_mmq_quantize");
+}
+
+TSX_API int tsx_moe_mmq_quantize_route(const float* x, void* xq, int type, int64_t cols, int64_t ld, int64_t rows,
+                                       const float* logits, int32_t* ids, float* weights, int n_expert, int k,
+                                       void* stream) {
+    (void) type;  // one layout serves every weight type
+    if (n_expert <= 0 || n_expert % 64 != 0 || n_expert > kMaxExpertsMmq || k < 1 || k > 16 || k > n_expert) {
+        set_error("tsx_moe_mmq_quantize_route: %d experts / top-%d not supported (a multiple of 64 up to 512, k 1..16)",
+                  n_expert, k);
+        return TSX_ERR_UNSUPPORTED;
+    }
+    TSX_REQUIRE(x && xq && logits && ids && weights && cols > 0 && cols % 32 == 0 && ld >= cols && ld % 4 == 0 &&
+                    rows >= 0 && aligned(xq, 256) && aligned(x, 16) && aligned(logits, 4) && aligned(ids, 4) &&
+                    aligned(weights, 4),
+                "tsx_moe_mmq_quantize_route: x (16-byte aligned, ld a multiple of 4), xq (256-byte aligned), cols a "
+                "multiple of 32, logits, ids, weights");
+    const MmqPlanes P = planes(xq, rows, cols);
+    const int qb = (int) ((rows * (cols / 4) + kThreads - 1) / kThreads);
+    const int rb = (int) ((rows + 3) / 4);
+    mmq_quantize_route_kernel<<<(unsigned) (qb + kPadBlocks + rb), kThreads, 0, (hipStream_t) stream>>>(
+        x, P, cols, ld, rows, qb, rb, logits, ids, weights, n_expert, k);
+    return launch_status("tsx_moe_mmq_quantize_route");
 }
 
 TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {

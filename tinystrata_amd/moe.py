@@ -195,13 +195,13 @@ class MoELayer:
     def _prefill_fused(self, x, logits, sgate, y):
         W, L, k, N, FF, T = self.W, self.W.L, self.k, self.N, self.FF, self.n_tok
         main = torch.cuda.current_stream()
-        ops.mmq_quantize(x, None, L.gu_type, N, N, T, xq=self.txq)  # every token once; routed rows read it via et
+        # every token's Q8_1 row once (routed rows read it via et) and the router's picks, in one launch
+        ops.mmq_quantize_route(x, L.gu_type, logits, k, xq=self.txq, ids=self.ids, wts=self.wts)
         if W.shared is not None:
             if self.side is None:
                 self.side = torch.cuda.Stream(device=x.device)
                 self.x_ready = torch.cuda.Event()
             self.x_ready.record(main)
-        ops.native_router_topk(logits, k, self.ids, self.wts)
         bounds, ed, et, rinv, mr = ops.route_sort(self.ids, k, W.n_expert, bufs=self.sort)
         ops.mmq_gate_up_swiglu(W.blobs, L.gu_type, FF, N, W.stride, W.n_expert, self.txq, T, et, bounds, self.n_ent,
                                hq=self.mhq)

@@ -219,6 +219,22 @@ def mmq_quantize(x, ids, ggml_type: int, cols: int, ld: int, rows: int, xq=None,
     return xq
 
 
+def mmq_quantize_route(x, ggml_type: int, logits, k: int, xq=None, ids=None, wts=None, stream=None):
+    """mmq_quantize of the token rows of x (ids None) and native_router_topk of logits in one launch; returns
+    (xq, ids, wts)."""
+    rows, cols = x.shape
+    n_expert = logits.shape[1]
+    if xq is None:
+        xq = torch.empty(mmq_q8_bytes(rows, cols), dtype=torch.uint8, device=x.device)
+    if ids is None:
+        ids = torch.empty((rows, k), dtype=torch.int32, device=x.device)
+    if wts is None:
+        wts = torch.empty((rows, k), dtype=torch.float32, device=x.device)
+    check(lib().tsx_moe_mmq_quantize_route(_p(x), _p(xq), ggml_type, cols, x.stride(0), rows, _p(logits), _p(ids),
+                                           _p(wts), n_expert, k, _stream(stream)), "mmq_quantize_route")
+    return xq, ids, wts
+
+
 def mmq_run(w, ggml_type: int, w_rows: int, w_cols: int, expert_bytes: int, n: int, xq, bounds, ids, total_rows: int,
             dst, ld_dst: int, max_rows: int = 0, stream=None) -> None:
     p = MmqProduct(w=_p(w), type=ggml_type, n=n, w_rows=w_rows, w_cols=w_cols, expert_bytes=expert_bytes, xq=_p(xq),
