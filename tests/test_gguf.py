@@ -161,7 +161,7 @@ def test_split_models(tmp_path):
     bad.write(names[1])
     with pytest.raises(_lib.TsxError) as e:
         GgufModel(names[0])
-    assert "does not declare itself shard 2" in str(e.value)
+    assert "shard 2 of 3" in str(e.value) and "does not match the set: split.no" in str(e.value)
     parts[1].write(names[1])
     parts[2].tensors.pop()
     parts[2].write(names[2])
@@ -171,10 +171,24 @@ def test_split_models(tmp_path):
     (tmp_path / "model-00003-of-00003.gguf").unlink()
     with pytest.raises(_lib.TsxError) as e:
         GgufModel(names[0])
-    assert e.value.rc == _lib.TSX_ERR_NOT_FOUND and "missing model shard" in str(e.value)
+    assert e.value.rc == _lib.TSX_ERR_NOT_FOUND and "1 of its 3 shard files not found" in str(e.value)
     with pytest.raises(_lib.TsxError) as e:
         GgufModel([names[0]])
-    assert "opened as a whole model" in str(e.value)
+    assert "is not a whole model" in str(e.value)
+
+
+def test_split_names(tmp_path):
+    # only "<stem>-NNNNN-of-MMMMM.gguf" with 1 <= NNNNN <= MMMMM names a split model; the stem may hold hyphens and
+    # digits of its own, and only the shard number changes between the shards' names
+    d = tmp_path / "snap-1-of-2"
+    d.mkdir()
+    names = [str(d / f"m-7-of-9-{i:05d}-of-00002.gguf") for i in (1, 2)]
+    for n in names:
+        GgufFile().kv("general.architecture", STRING, "x").write(n)
+    assert split_paths(names[1]) == names
+    for odd in ("m-0001-of-00002.gguf", "m-00003-of-00002.gguf", "m-00000-of-00002.gguf", "m-00001-of-00002.GGUF",
+                "m-00001-of-00002.gguf.part", "-00001-of-00002.gguf"):
+        assert split_paths(str(d / odd)) == [str(d / odd)]
 
 
 def expert_file(gu, dn, n_embd, n_ff, n_exp, seed, shared=True, layer=3):

@@ -1,8 +1,9 @@
 // tsx_gguf.cpp - GGUF v3 models for the expert kernels: every shard mapped read-only, the header parsed through a
 // bounds-checked cursor, and one layer's routed experts repacked into the [gate | up | down] blobs.
 //
-// Behaviour follows the reference reader (include/strata/artifact/gguf_reader.hpp:233-666) and its shard naming
-// (include/strata/artifact/gguf_split.hpp:25-55); the repack follows the engine's loader
+// Behaviour follows the reference reader (include/strata/artifact/gguf_reader.hpp:233-666); split models use
+// llama.cpp's gguf-split file names and split.* keys, as the reference does (include/strata/artifact/gguf_split.hpp:
+// 19-23, gguf_reader.hpp:579-607), parsed and checked here by code of this file's own; the repack follows the engine's loader
 // (src/qwen35/q36_engine.cu:1144-1168, expert_blob :1196-1201).  The host copies the three strided parts of every
 // blob straight from the mapping with hipMemcpy2DAsync, one call per part for a whole run of experts.
 #include <fcntl.h>
@@ -18,6 +19,7 @@
 #include <map>
 #include <memory>
 #include <numeric>
+#include <regex>
 #include <string>
 #include <vector>
 
@@ -172,9 +174,11 @@ struct Shard {
         const auto it = meta.find(k);
         return it == meta.end() ? nullptr : &it->second;
     }
+    // the tensor's payload [data_start + offset, + bytes) ends within the mapping, with no wrap of the sum
     bool inside(const Tensor& t) const {
-        const uint64_t payload = size - data_start;
-        return t.bytes != 0 && t.offset <= payload && t.bytes <= payload - t.offset;
+        uint64_t at = 0, end = 0;
+        if (t.bytes == 0 || __builtin_add_overflow(data_start, t.offset, &at)) return false;
+        return !__builtin_add_overflow(at, t.bytes, &end) && end <= size;
     }
 
     void open_map() {
@@ -230,30 +234,49 @@ struct Shard {
     }
 };
 
-// the shard paths of the model `any` belongs to: <stem>-NNNNN-of-MMMMM.gguf, else `any` alone
+// A split model's file names, as llama.cpp's gguf-split writes them: "<stem>-<index>-of-<count>.gguf" with both
+// numbers five digits wide, index 1-based.  parse_split_name takes one such name apart; names of every other form
+// belong to models of one file.
+struct SplitName {
+    std::string stem;  // everything before "-<index>-of-"
+    int index = 0, count = 0;
+    std::string name(int i) const {
+        char digits[32];
+        std::snprintf(digits, sizeof digits, "-%05d-of-%05d.gguf", i, count);
+        return stem + digits;
+    }
+};
+bool parse_split_name(const std::string& path, SplitName& out) {
+    // the file name itself must have a stem: "dir/-00001-of-00002.gguf" is a one-file model
+    static const std::regex form(R"(^([^/]+)-([0-9]{5})-of-([0-9]{5})\.gguf$)");
+    const size_t slash = path.find_last_of('/');
+    const std::string dir = slash == std::string::npos ? std::string() : path.substr(0, slash + 1);
+    const std::string file = slash == std::string::npos ? path : path.substr(slash + 1);
+    std::smatch m;
+    if (!std::regex_match(file, m, form)) return false;
+    out.stem = dir + m[1].str();
+    out.index = std::stoi(m[2].str());
+    out.count = std::stoi(m[3].str());
+    return out.count >= 1 && out.index >= 1 && out.index <= out.count;
+}
+bool readable_file(const std::string& p) {
+    struct stat st {};
+    return ::stat(p.c_str(), &st) == 0 && S_ISREG(st.st_mode) && ::access(p.c_str(), R_OK) == 0;
+}
+// every shard of the model `any` belongs to, first shard first; `any` alone when its name is not a split name
 std::vector<std::string> split_paths(const std::string& any) {
-    const size_t at = any.rfind("-of-");
-    if (at == std::string::npos || at < 6 || any[at - 6] != '-' || any.size() != at + 4 + 5 + 5 ||
-        any.compare(at + 9, 5, ".gguf") != 0)
-        return {any};
-    int no = 0, n = 0;
-    for (size_t i = 0; i < 5; ++i) {
-        const char a = any[at - 5 + i], b = any[at + 4 + i];
-        if (a < '0' || a > '9' || b < '0' || b > '9') return {any};
-        no = no * 10 + (a - '0');
-        n = n * 10 + (b - '0');
-    }
-    if (n < 1 || no < 1 || no > n) return {any};
+    SplitName sn;
+    if (!parse_split_name(any, sn)) return {any};
     std::vector<std::string> out;
-    for (int i = 1; i <= n; ++i) {
-        char num[8];
-        std::snprintf(num, sizeof num, "%05d", i);
-        std::string p = any;
-        p.replace(at - 5, 5, num);
-        if (access(p.c_str(), R_OK) != 0)
-            throw Fault{"missing model shard " + p + " (shard " + std::to_string(i) + " of " + std::to_string(n) + ")"};
-        out.push_back(std::move(p));
+    std::string absent;
+    int n_absent = 0;
+    for (int i = 1; i <= sn.count; ++i) {
+        out.push_back(sn.name(i));
+        if (!readable_file(out.back()) && n_absent++ == 0) absent = out.back();
     }
+    if (n_absent)
+        throw Fault{"split model " + sn.stem + ": " + std::to_string(n_absent) + " of its " + std::to_string(sn.count) +
+                    " shard files not found, first " + absent};
     return out;
 }
 
@@ -271,31 +294,48 @@ struct tsx_gguf {
     std::vector<std::pair<int, size_t>> order;         // directory order: (shard, tensor)
     std::map<std::string, std::pair<int, size_t>> by;  // name -> (shard, tensor)
 
-    void validate_split() const {
-        const size_t n = shards.size();
-        const Meta* count0 = shards[0]->get("split.count");
+    // The split.* keys must describe exactly the shard set that was opened: every shard says "n shards, I am number
+    // i" (split.no counts from 0), all of them quote one tensor total (split.tensors.count, optional) and their
+    // directories add up to it, and the model metadata sits in the first shard.  A lone file may not claim to be
+    // part of a larger set.
+    void check_split() const {
+        constexpr uint64_t kNone = ~0ull;
+        auto declared = [](const Shard& s, const char* key) {
+            const Meta* m = s.get(key);
+            return m ? m->u : kNone;
+        };
+        auto show = [](uint64_t v) { return v == kNone ? std::string("absent") : std::to_string(v); };
+        const uint64_t n = shards.size();
         if (n == 1) {
-            if (count0 && count0->u > 1)
-                throw Fault{shards[0]->path + " is shard 1 of " + std::to_string(count0->u) +
-                            ", but it was opened as a whole model"};
+            const uint64_t claim = declared(*shards[0], "split.count");
+            if (claim != kNone && claim > 1)
+                throw Fault{shards[0]->path + ": split.count is " + std::to_string(claim) +
+                            ", so this file alone is not a whole model (open it by its path to find the other shards)"};
             return;
         }
-        if (!shards[0]->get("general.architecture"))
-            throw Fault{shards[0]->path + " has no general.architecture; the first shard of a split model carries "
-                                          "the metadata"};
-        const Meta* total = shards[0]->get("split.tensors.count");
-        uint64_t tensors = 0;
-        for (size_t i = 0; i < n; ++i) {
+        const uint64_t total = declared(*shards[0], "split.tensors.count");
+        uint64_t listed = 0;
+        for (uint64_t i = 0; i < n; ++i) {
             const Shard& s = *shards[i];
-            const Meta *count = s.get("split.count"), *no = s.get("split.no"), *tc = s.get("split.tensors.count");
-            if (!count || !no || count->u != n || no->u != i || (total && (!tc || tc->u != total->u)))
-                throw Fault{s.path + " does not declare itself shard " + std::to_string(i + 1) + " of " +
-                            std::to_string(n) + " of this model (split.count / split.no / split.tensors.count)"};
-            tensors += s.tensors.size();
+            std::string bad;
+            if (declared(s, "split.count") != n)
+                bad = "split.count " + show(declared(s, "split.count")) + ", expected " + std::to_string(n);
+            else if (declared(s, "split.no") != i)
+                bad = "split.no " + show(declared(s, "split.no")) + ", expected " + std::to_string(i);
+            else if (declared(s, "split.tensors.count") != total)
+                bad = "split.tensors.count " + show(declared(s, "split.tensors.count")) + " where the first shard has " +
+                      show(total);
+            if (!bad.empty())
+                throw Fault{"shard " + std::to_string(i + 1) + " of " + std::to_string(n) + " (" + s.path +
+                            ") does not match the set: " + bad};
+            listed += s.tensors.size();
         }
-        if (total && tensors != total->u)
-            throw Fault{"the " + std::to_string(n) + " shards hold " + std::to_string(tensors) +
-                        " tensors, but split.tensors.count is " + std::to_string(total->u)};
+        if (total != kNone && listed != total)
+            throw Fault{"split model: split.tensors.count is " + std::to_string(total) + " but the " +
+                        std::to_string(n) + " shard directories list " + std::to_string(listed) + " tensors"};
+        if (!shards[0]->get("general.architecture"))
+            throw Fault{shards[0]->path + ": first shard of a split model without general.architecture (the model "
+                                          "metadata belongs there)"};
     }
     void fill(int shard, size_t i, tsx_gguf_tensor* out) const {
         const Shard& s = *shards[shard];
@@ -353,7 +393,7 @@ TSX_API int tsx_gguf_open(const char* const* paths, int n_paths, tsx_gguf** out)
             s->parse();
             g->shards.push_back(std::move(s));
         }
-        g->validate_split();
+        g->check_split();
         for (int i = 0; i < (int) g->shards.size(); ++i)
             for (size_t t = 0; t < g->shards[i]->tensors.size(); ++t) {
                 const std::string& name = g->shards[i]->tensors[t].name;
