@@ -54,7 +54,7 @@ def test_q8_0_closed_form():
 # ------------------------------------------------------------------ Q8_1
 def test_q8_1_closed_form():
     rng = np.random.default_rng(4)
-    x = rng.normal(0, 2, (3, 64)).astype(np.float32)
+    x = rng.normal(0, 2, (512, 2048)).astype(np.float32)
     d, s, codes = O.q8_1_split(O.quantize_q8_1(x))
     xb = x.reshape(-1, 32)
     amax = np.abs(xb).max(1)
@@ -64,7 +64,19 @@ def test_q8_1_closed_form():
     r = xb / dd[:, None]
     exp = np.sign(r) * np.floor(np.abs(r) + 0.5)
     assert (codes == np.clip(exp, -127, 127)).all()
-    assert np.allclose(s, xb.sum(1), rtol=2e-3, atol=1e-3)
+    # s, exactly: the fp16 of the 32 raw values' float sum in the warp's xor-tree order (q8_1_store,
+    # src/kernels/cuda/iq_kernels.cu:1469-1474: sum += shfl_xor(sum, o) for o = 16 .. 1), clamped to the largest half
+    v, lanes = xb.copy(), np.arange(32)
+    for o in (16, 8, 4, 2, 1):
+        v = (v + v[:, lanes ^ o]).astype(np.float32)
+    assert (v == v[:, :1]).all()  # every lane of the tree ends with the same bits
+    tree = np.clip(v[:, 0], -65504, 65504).astype(np.float16).astype(np.float32)
+    assert (s == tree).all()
+    # the check tells summation orders apart: a left-to-right float sum rounds to another half in some blocks
+    seq = np.zeros(len(xb), np.float32)
+    for j in range(32):
+        seq = (seq + xb[:, j]).astype(np.float32)
+    assert (seq.astype(np.float16).astype(np.float32) != tree).sum() > 0
 
 
 def test_q8_1_special_blocks():
@@ -262,3 +274,82 @@ def test_layer_modes_agree_for_q8_0():
     assert (ids == ids1).all()
     rel = np.linalg.norm(y0 - y1) / np.linalg.norm(y1)
     assert rel < 1e-3, rel
+
+
+def _ref_act(t: int, v: np.ndarray) -> np.ndarray:
+    """The reference CPU's activation for weight type t (IQ3 / Q4_K: Q8_K by q8k_quant_avx2 itself)."""
+    v = np.ascontiguousarray(v, np.float32)
+    a = np.empty(v.size // 256 * 292, np.uint8)
+    O.ref().ref_q8k_quant(v.ctypes.data, a.ctypes.data, v.size)
+    return a
+
+
+def _ref_rows(t, w, n, rows, a):
+    w = np.ascontiguousarray(w)
+    y = np.empty(rows, np.float32)
+    assert O.ref().ref_rows(t, w.ctypes.data, n, rows, a.ctypes.data, 1, y.ctypes.data) == 0
+    return y
+
+
+def _ref_layer(L, x, ids, wts, k, blobs, shared, sgate, plant=None):
+    """A MoE layer assembled from the reference's own CPU kernels (oracle/_ref), in the structure of
+    src/lfm2/cpu_experts.cpp:145-235: Q8_K of x, the gate/up rows with SwiGLU inside (iq512/kq256_gu_rows), Q8_K of h,
+    the down rows, and the combine in pick order (w0 p0, then fma; + sigmoid(sgate) * shared).  `plant` swaps in one
+    plausible mistake, to show the comparison catches it."""
+    N, FF = int(L.n_embd), int(L.n_ff)
+    up, down = int(L.up_off), int(L.down_off)
+
+    def expert(blob, xt):
+        a = _ref_act(L.gu_type, xt)
+        if plant == "swiglu_order":  # silu(up) * gate, from the reference's plain rows
+            g, u = _ref_rows(L.gu_type, blob[:up], N, FF, a), _ref_rows(L.gu_type, blob[up:down], N, FF, a)
+            h = ((u / (1 + np.exp(-u.astype(np.float64)))) * g).astype(np.float32)
+        else:
+            h = np.empty(FF, np.float32)
+            assert O.ref().ref_gu_rows(L.gu_type, np.ascontiguousarray(blob).ctypes.data, N, FF, a.ctypes.data, 1,
+                                       h.ctypes.data) == 0
+        if plant == "h_q8_1":  # the down rows on h's Q8_1 image (the GPU contract's), not the reference CPU's Q8_K
+            return O.mmvq_q8_1(L.d_type, np.ascontiguousarray(blob[down:]), FF, N, O.quantize_q8_1(h[None]), 1).ravel()
+        return _ref_rows(L.d_type, blob[down:], FF, N, _ref_act(L.d_type, h))
+
+    T = x.shape[0]
+    y = np.zeros((T, N), np.float32)
+    for t in range(T):
+        p = [expert(blobs[ids[t, j]], x[t]) for j in range(k)]
+        acc = (wts[t, 0] * p[0]).astype(np.float32)
+        for j in range(1, k):  # fmaf in float64: the product is exact, one rounding of the sum to float32
+            acc = (wts[t, j].astype(np.float64) * p[j] + acc).astype(np.float32)
+        if shared is not None:
+            gs = np.float32(1.0) if plant == "shared_gate" else np.float32(1 / (1 + np.exp(-np.float64(sgate[t]))))
+            acc = (acc + gs * expert(shared, x[t])).astype(np.float32)
+        y[t] = acc
+    return y
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built here")
+@pytest.mark.parametrize("gu,dn,N,FF,shared", [(O.IQ3_XXS, O.IQ3_S, 1024, 512, True),
+                                               (O.Q4_K, O.Q4_K, 1024, 256, False)])
+def test_layer_composition_against_reference_rows(gu, dn, N, FF, shared):
+    """orc_moe_layer in the reference CPU's activation mode against the same layer built from oracle/_ref's own
+    kernels: pins the SwiGLU operand order, the quantization of h and the shared expert's gate directly, not only
+    through their parts.  The two differ by float summation order alone (rows, SwiGLU), so the bound is 1e-5 relative
+    L2; each planted mistake moves the layer by more than 1e-2."""
+    from tinystrata_amd import moe, ops
+
+    E, k, T = 16, 4, 3
+    Lp = ops.native_expert_layout(gu, dn, N, FF)
+    L = O.layout(gu, dn, N, FF)
+    pool = moe.synthetic_pool(Lp, 6, seed=9)
+    blobs = pool[(np.arange(E) * 5 + 1) % 5]
+    sh = pool[5] if shared else None
+    rng = np.random.default_rng(17)
+    x = rng.normal(0, 1, (T, N)).astype(np.float32)
+    logits = rng.normal(0, 1, (T, E)).astype(np.float32)
+    sg = rng.normal(0, 1, T).astype(np.float32) if shared else None
+    y, ids, w = O.moe_layer(1, L, x, logits, k, blobs, pool.shape[1], sh, sg)
+    ref = _ref_layer(Lp, x, ids, w, k, blobs, sh, sg)
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    assert rel < 1e-5, rel
+    for plant in ("swiglu_order", "h_q8_1") + (("shared_gate",) if shared else ()):
+        bad = _ref_layer(Lp, x, ids, w, k, blobs, sh, sg, plant=plant)
+        assert np.linalg.norm(y - bad) / np.linalg.norm(ref) > 1e-2, plant
