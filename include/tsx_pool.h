@@ -79,13 +79,15 @@ TSX_API int tsx_pool_host_works(const tsx_pool* p);
  * running the batch: the jobs and their buffers must stay valid until tsx_pool_destroy has returned.
  * Replaces ExpertPool::run_split_multi_native (pool.hpp:139; src/kernels/cpu/pool.cpp:773-817). */
 TSX_API int tsx_pool_run(tsx_pool* p, const tsx_cpu_fmt* f, const tsx_cpu_job* jobs, int n);
-/* Accumulated milliseconds: [0] waiting for parked workers, [1] draining, [2] phases gate/up, [3] quantize h,
- * [4] down, [5] fused batches; and *bytes = expert blob bytes evaluated.  Replaces ExpertPool::phase_ms and the
- * ms_multi_* counters (pool.hpp:140-143,160-167). */
+/* Accumulated milliseconds: [0] the host waiting for workers to leave the slot it is about to reuse, [1] the host
+ * from publishing a batch until its last chunk finished, [2] gate/up row chunks, [3] quantizing h, [4] down row
+ * chunks (2-4 summed over every thread), [5] threads waiting for an h another thread is making; and *bytes = expert
+ * blob bytes evaluated.  Replaces ExpertPool::phase_ms and the ms_multi_* counters (pool.hpp:140-143,160-167). */
 TSX_API int tsx_pool_stats(const tsx_pool* p, double* ms6, int64_t* bytes);
-/* The pool's state as one line of text into buf (n bytes, truncated): the epoch, the head word's epoch / jobs /
- * next index, done, parked, sleepers, and each worker's state (parked, sleeping, between batches, or the job it
- * runs).  Safe to call from any thread at any time.  Replaces ExpertPool::diag (pool.hpp:118-119,
+/* The pool's state as one line of text into buf (n bytes, truncated): the current batch's sequence number, its
+ * experts, finished / total and unclaimed chunks, the workers attached to each of the two slots, idle workers and
+ * sleepers, FAILED after a stall, and each worker's state (idle, sleeping, waiting-h, or the expert it works on).
+ * Safe to call from any thread at any time.  Replaces ExpertPool::diag (pool.hpp:118-119,
  * src/kernels/cpu/pool.cpp:457-476). */
 TSX_API int tsx_pool_diag(const tsx_pool* p, char* buf, size_t n);
 /* How long a parked worker spins before it sleeps, in microseconds (default 20000): a test knob, as the reference's
@@ -99,7 +101,9 @@ TSX_API int tsx_pool_set_stall_ms(tsx_pool* p, int64_t ms);
  * form): entries e = t*k + j of ids[n_tok][k] whose expert has slot_of[x] < 0 are the misses.  Each missed
  * token's x row (n_embd floats) is quantized once; jobs take up to TSX_CPU_MAXT tokens of one expert; miss i
  * (in entry order) writes row i of cpu_out (n_embd floats).  miss[e] = i for a miss, -1 for a resident entry;
- * *n_miss = the count.  host_blobs: every expert's blob, `stride` bytes apart, in host memory. */
+ * *n_miss = the count.  host_blobs: every expert's blob, `stride` bytes apart, in host memory.  After
+ * TSX_ERR_STALLED, workers may still be running the stalled batch, reading host_blobs and the quantized x and
+ * writing cpu_out: host_blobs and cpu_out must stay valid until tsx_pool_destroy has returned. */
 TSX_API int tsx_moe_hybrid_cpu(tsx_pool* p, const tsx_cpu_fmt* f, const uint8_t* host_blobs, uint64_t stride,
                                const int32_t* slot_of, int n_expert, int k, int n_tok, const int32_t* ids,
                                const float* x, float* cpu_out, int32_t* miss, int32_t* n_miss);
@@ -109,7 +113,9 @@ TSX_API int tsx_moe_hybrid_cpu(tsx_pool* p, const tsx_cpu_fmt* f, const uint8_t*
  * the resident entries grouped into their slots and run, the shared expert; then the host waits for the ids and x
  * alone and runs the misses on the pool while the GPU works, uploads the CPU rows and the miss map, merges them
  * into `parts` and enqueues the combine (y += ...).  Returns after the last enqueue; n_miss is written.  The pinned
- * buffers are reused by the next call on the same stream (its copies run after this call's uploads). */
+ * buffers are reused by the next call on the same stream (its copies run after this call's uploads).  After
+ * TSX_ERR_STALLED, workers may still be running the stalled batch: host_blobs and h_rows must stay valid until
+ * tsx_pool_destroy has returned. */
 typedef struct tsx_hybrid_layer {
     tsx_expert_layout L;
     int32_t n_expert, k, n_tok, sg_stride;

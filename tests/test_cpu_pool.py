@@ -191,8 +191,9 @@ def test_pool_stall_is_an_error_not_a_hang():
 
 def test_hybrid_cpu_stall_then_destroy():
     """A stall inside tsx_moe_hybrid_cpu: the call returns TSX_ERR_STALLED, the next call is refused before it touches
-    the pool's token rows (which the stalled batch's worker may still read), and destroying the pool joins that worker
-    while the job table it reads is still the pool's own copy."""
+    the pool's token rows (which the stalled batch's worker may still read), the caller's blobs and output rows stay
+    referenced by the pool (the stalled worker may still read and write them), and destroying the pool joins that
+    worker and only then lets them go."""
     N, FF, E, k, T = 2048, 512, 4, 4, 8
     f = cpu_fmt(Q8_0, Q8_0, N, FF)
     blobs = experts(Q8_0, Q8_0, N, FF, E, seed=7)
@@ -211,4 +212,7 @@ def test_hybrid_cpu_stall_then_destroy():
         hybrid_cpu(p, f, blobs, blobs.shape[1], slot_of, k, ids, x, rows, miss)
     assert e.value.rc == _lib.TSX_ERR_STALLED and "takes no more work" in str(e.value)
     assert "FAILED" in p.diag()
+    # the stalled call's arrays are held until close(): its worker may still be reading blobs and writing rows
+    assert any(held[0] is blobs and held[2] is rows for held in p._stalled)
     p.close()
+    assert p._stalled == []

@@ -23,8 +23,10 @@
 //   * Idle workers spin with a pause, yield now and then, and after `spin_us_` sleep on a futex word the host bumps on
 //     every publish; a sleeper count spares the system call while nobody sleeps.
 //   * Every host wait is bounded by `stall_ms_`: a batch that makes no progress for that long marks the pool failed,
-//     the call returns TSX_ERR_STALLED and the pool takes no further work.  The job table lives in the slot, so a
-//     worker still busy with a stalled batch reads the pool's memory, not the caller's.
+//     the call returns TSX_ERR_STALLED and the pool takes no further work.  The job table lives in the slot, but the
+//     pointers in it are the caller's: a worker still busy with a stalled batch may go on reading the weight blobs
+//     and activations and writing the output rows, so after a stall every buffer of that batch must stay valid until
+//     tsx_pool_destroy has joined the workers.
 //
 // The row decomposition changes no result: every output row is one tsx_cpu_gu_rows / tsx_cpu_down_rows row, whichever
 // thread computes it, and h is quantized from complete rows.

@@ -154,8 +154,13 @@ def hybrid_cpu(pool: ExpertPool, f: CpuFmt, host_blobs: np.ndarray, stride: int,
     ids = np.ascontiguousarray(ids, np.int32)
     x = np.ascontiguousarray(x, np.float32)
     nm = C.c_int32()
-    check(lib().tsx_moe_hybrid_cpu(pool.handle, C.byref(f), _ptr(host_blobs), stride, _ptr(slot_of), len(slot_of), k,
-                                   n_tok, _ptr(ids), _ptr(x), _ptr(cpu_out), _ptr(miss), C.byref(nm)), "hybrid_cpu")
+    rc = lib().tsx_moe_hybrid_cpu(pool.handle, C.byref(f), _ptr(host_blobs), stride, _ptr(slot_of), len(slot_of), k,
+                                  n_tok, _ptr(ids), _ptr(x), _ptr(cpu_out), _ptr(miss), C.byref(nm))
+    if rc == TSX_ERR_STALLED:
+        # workers of the stalled batch may still read the blobs and the activations and write cpu_out: they stay
+        # alive until the pool's close() has joined the workers, as ExpertPool.run keeps its arrays
+        pool._stalled.append((host_blobs, x, cpu_out, miss, ids, slot_of))
+    check(rc, "hybrid_cpu")
     return nm.value
 
 
@@ -233,6 +238,10 @@ class HybridMoELayer:
         A = self.args
         A.x, A.logits, A.y = x.data_ptr(), logits.data_ptr(), y.data_ptr()
         A.sgate = sgate.data_ptr() if sgate is not None else None
-        check(lib().tsx_moe_hybrid_decode_layer(self.pool.handle, C.byref(self.f), C.byref(A),
-                                                torch.cuda.current_stream(y.device).cuda_stream), "hybrid layer")
+        rc = lib().tsx_moe_hybrid_decode_layer(self.pool.handle, C.byref(self.f), C.byref(A),
+                                               torch.cuda.current_stream(y.device).cuda_stream)
+        if rc == TSX_ERR_STALLED:
+            # the stalled batch's workers may still read the host blobs and x and write the CPU rows
+            self.pool._stalled.append((self.host_blobs, self.h_x, self.h_rows))
+        check(rc, "hybrid layer")
         self.n_miss = A.n_miss
