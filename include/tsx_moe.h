@@ -155,8 +155,10 @@ TSX_API int tsx_moe_decode_layer(const tsx_expert_layout* L, const void* blobs, 
 /* tsx_moe_decode_layer without a scratch argument, for callers that cannot allocate device memory (code under HIP
  * graph capture, serving loops that allocate nothing after start-up, harnesses that forbid hipMalloc).  No counterpart
  * in the reference.  The scratch is a fixed device array of tsx_moe_decode_layer_noalloc_max_bytes() (128 KiB) per
- * GPU, held until the process ends; its address is looked up once per device (with that device current) on the first
- * call.  A call needing more scratch than that (tsx_moe_decode_layer_scratch_bytes) returns TSX_ERR_UNSUPPORTED.
+ * GPU, held until the process ends; its address is looked up once per device (with that device current), by
+ * tsx_moe_init when it can (a failure there is ignored) and otherwise on the first call, which then returns the
+ * runtime's hipError_t if the lookup fails.  A call needing more scratch than that
+ * (tsx_moe_decode_layer_scratch_bytes) returns TSX_ERR_UNSUPPORTED.
  * Nothing is allocated or freed.  Calls share their GPU's array: calls that overlap on one GPU (other streams, other
  * threads) race; calls in one stream's order do not. */
 TSX_API size_t tsx_moe_decode_layer_noalloc_max_bytes(void);

@@ -47,15 +47,20 @@ def test_noalloc_matches_allocating_entry_point():
     W = moe.weights_from_pool(L, dev(p), E, order, 7)
     rng = np.random.default_rng(21)
     assert lib().tsx_moe_decode_layer_noalloc_max_bytes() >= ops.decode_layer_scratch_bytes(8, 8, 1024)
-    for T in (8, 3):  # the second call smaller: the array keeps the first call's contents
+    W0 = moe.MoEWeights(L=W.L, n_expert=W.n_expert, stride=W.stride, blobs=W.blobs, shared=None)
+    # each call smaller than the one before it, so the array holds an earlier call's bytes: T = 1 is the one-token
+    # launch A (fp32 h quantized by launch B, tables written by its last block) over what the 8-token call left, with
+    # and without the shared expert
+    for T, Wt in ((8, W), (1, W), (3, W), (1, W0)):
         x = dev(rng.normal(0, 1, (T, N)).astype(np.float32))
         logits = dev(rng.normal(0, 1, (T, E)).astype(np.float32))
-        sg = dev(rng.normal(0, 1, T).astype(np.float32))
-        (ya, ia, wa), (yb, ib, wb) = _both(L, W, k, x, logits, sg)
+        sg = dev(rng.normal(0, 1, T).astype(np.float32)) if Wt.shared is not None else None
+        (ya, ia, wa), (yb, ib, wb) = _both(L, Wt, k, x, logits, sg)
+        tag = (T, Wt.shared is not None)
         assert np.isfinite(ya).all() and (ia >= 0).all()
-        assert (ia == ib).all() and (wa.view(np.uint32) == wb.view(np.uint32)).all(), T
-        assert (ya.view(np.uint32) == yb.view(np.uint32)).all(), T
-        print(f"noalloc T={T}: bit-identical to the allocating entry point")
+        assert (ia == ib).all() and (wa.view(np.uint32) == wb.view(np.uint32)).all(), tag
+        assert (ya.view(np.uint32) == yb.view(np.uint32)).all(), tag
+        print(f"noalloc T={T} shared={tag[1]}: bit-identical to the allocating entry point", flush=True)
 
 
 def test_noalloc_refuses_what_does_not_fit():

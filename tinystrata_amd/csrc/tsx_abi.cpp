@@ -39,8 +39,12 @@ TSX_API int tsx_moe_init(int device) {
         tsx::set_error("tsx_moe_init(%d): %s", device, hipGetErrorString(e));
         return (int) e;
     }
-    // the no-allocation decode layer's scratch address on this device, looked up now rather than on its first call
-    if (!tsx::noalloc_scratch_ptr()) return TSX_ERR_ARG;
+    // the no-allocation decode layer's scratch address on this device, looked up now rather than on its first call;
+    // best effort: only tsx_moe_decode_layer_noalloc needs it, and that call looks it up again and reports a failure
+    if (!tsx::noalloc_scratch_ptr(nullptr)) {
+        (void) hipGetLastError();  // the runtime's error state stays clear for the caller's next HIP call
+        tsx::clear_error();
+    }
     return TSX_OK;
 }
 

@@ -22,7 +22,7 @@ inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t) p % a) == 
 
 // The current device's address of the no-allocation decode layer's scratch array (tsx_layer.hip); nullptr, with the
 // error recorded, when the runtime refuses the lookup.
-void* noalloc_scratch_ptr();
+void* noalloc_scratch_ptr(int* rc);
 
 #define TSX_REQUIRE(cond, ...)                  \
     do {                                        \

@@ -843,11 +843,14 @@ void* g_noalloc_ptr[kMaxDevices] = {};
 }  // namespace
 
 // The current device's address of noalloc_scratch (looked up once per device, with that device current); nullptr
-// with the error recorded when the runtime refuses.
-void* noalloc_scratch_ptr() {
+// with the error recorded and *rc set (the hipError_t, or TSX_ERR_UNSUPPORTED for a device index past the table)
+// when the runtime refuses.
+void* noalloc_scratch_ptr(int* rc) {
     int device = -1;
-    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+    const hipError_t ge = hipGetDevice(&device);
+    if (ge != hipSuccess || device < 0 || device >= kMaxDevices) {
         set_error("tsx_moe_decode_layer_noalloc: no current device (or one past the first %d)", kMaxDevices);
+        if (rc) *rc = ge != hipSuccess ? (int) ge : (int) TSX_ERR_UNSUPPORTED;
         return nullptr;
     }
     std::lock_guard<std::mutex> lk(g_noalloc_mu);
@@ -857,6 +860,7 @@ void* noalloc_scratch_ptr() {
         if (e != hipSuccess || p == nullptr) {
             set_error("tsx_moe_decode_layer_noalloc: hipGetSymbolAddress on device %d: %s", device,
                       hipGetErrorString(e));
+            if (rc) *rc = e != hipSuccess ? (int) e : (int) hipErrorInvalidSymbol;
             return nullptr;
         }
         g_noalloc_ptr[device] = p;
@@ -1028,8 +1032,9 @@ TSX_API int tsx_moe_decode_layer_noalloc(const tsx_expert_layout* Lp, const void
                   n_tok, k, (long long) Lp->n_ff, need, kNoAllocScratchBytes);
         return TSX_ERR_UNSUPPORTED;
     }
-    void* p = noalloc_scratch_ptr();
-    if (!p) return TSX_ERR_ARG;
+    int rc = TSX_OK;
+    void* p = noalloc_scratch_ptr(&rc);
+    if (!p) return rc;
     // every word launch B reads of the scratch is written by launch A of the same call first: nothing to clear
     return tsx_moe_decode_layer(Lp, blobs, stride, n_expert, k, n_tok, logits, x, shared, sgate, sg_stride, y, ids, wts,
                                 p, stream);
