@@ -327,12 +327,14 @@ __device__ __forceinline__ void i8_to_h(uint32_t w, uint32_t& lo, uint32_t& hi) 
     lo = hadd(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), 0xE480E480u);
     hi = hadd(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u), 0xE480E480u);
 }
-// four bytes in [0, 15] times the pair sc -> two fp16 pairs: (1024 + b) * sc - 1024 * sc, exact in one fma
+// four bytes in [0, 15] times the pair sc -> two fp16 pairs: (1024 + b) * sc - 1024 * sc, exact only as one fused
+// multiply-add (the product alone, up to 1039 * 63, would round in fp16), so the fma is explicit rather than left to
+// contraction
 __device__ __forceinline__ void nib_to_h(uint32_t w, h2 sc, h2 nsc, uint32_t& lo, uint32_t& hi) {
     const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u));
     const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u));
-    lo = __builtin_bit_cast(uint32_t, a * sc + nsc);
-    hi = __builtin_bit_cast(uint32_t, b * sc + nsc);
+    lo = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(a, sc, nsc));
+    hi = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(b, sc, nsc));
 }
 // the LDS address of p held in a register the compiler cannot see into, so that constant offsets from it go into
 // the 16-bit offset field of the LDS instructions instead of an add per access
