@@ -12,6 +12,9 @@ Default: the decode MoE layer stack of BASELINE.json configs[1].  A step is one 
 Inputs are synthetic (N(0,0.02) weights quantized by this library, N(0,1) activations, N(0,1) router logits with the
 config's skew) and resident in HBM before the timed region.  Prints one JSON line: the driver's contract plus the
 roofline of the dominant launch (timed with HIP events on its stream) and the reference CPU path timed on this host.
+The default decode line carries a "secondary" block with the other four BASELINE configurations measured the same
+way, each with its roofline and CPU baseline; the verify step also times its tokens through the one-token layer one
+at a time ("per_token").
 """
 from __future__ import annotations
 
@@ -30,6 +33,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "MoE layer tokens/s; decode HBM GB/s and prefill int8-MFMA % of peak"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+F16_PEAK_TFLOPS = 2500.0       # MI355X dense f16 MFMA: the engine the prompt products run on
 
 CONFIGS = {
     "decode": dict(gu=18, d=21, N=2048, FF=512, E=256, k=8, shared=True, T=1, layers=40, route="normal",
@@ -79,6 +83,8 @@ def parse_args(argv=None):
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prompt-chunk configurations measured after the default decode line")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--secondary-cpu-seconds", type=float, default=4.0,
+                    help="CPU baseline sample of each secondary configuration")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="before the timed region, run one plain fp32 copy kernel (out = in * 1) over this many MiB: "
                          "the known-size launch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
@@ -113,23 +119,31 @@ def main() -> int:
         "cpu_baseline": res["cpu_baseline"],
     }
     if args.config == "decode" and not args.no_secondary:
-        # the metric's prefill half: the prompt configurations, each measured the same way (fewer layers and steps;
-        # not part of `value`)
+        # every other BASELINE configuration, each measured the same way (not part of `value`): the metric's prefill
+        # half (the prompt chunks, fewer layers and steps), the Q8_0 plumbing layer and the speculative verify step
+        # (with the same tokens through the one-token layer one at a time beside it)
         sec = {}
-        for name in ("prefill_long", "prefill"):
-            r = run_config(args, name, CONFIGS[name], steps=8, warmup=2, cpu=False, layers=2)
-            sec[name] = {"workload": r["config"]["workload"], "value": r["value"], "unit": "MoE-layer tokens/s",
-                         "ms_per_step": r["ms_per_step"], "layer_us": r["config"]["layer_us"],
-                         "layer_hbm_frac": r["config"]["layer_hbm_frac"],
-                         "layer_int8_mfma_frac": r["config"]["layer_int8_mfma_frac"],
-                         "distinct_experts_per_layer": r["config"]["distinct_experts_per_layer"],
-                         "roofline": r["roofline"]}
+        for name, kw in (("prefill_long", dict(steps=8, warmup=2, layers=2)),
+                         ("prefill", dict(steps=8, warmup=2, layers=2)),
+                         ("plumb", dict(steps=10, warmup=3)),
+                         ("verify", dict(steps=10, warmup=3))):
+            r = run_config(args, name, CONFIGS[name], cpu=not args.no_cpu, cpu_seconds=args.secondary_cpu_seconds,
+                           **kw)
+            c = r["config"]
+            sec[name] = {"workload": c["workload"], "value": r["value"], "unit": "MoE-layer tokens/s",
+                         "ms_per_step": r["ms_per_step"], "layers": c["layers"], "layer_us": c["layer_us"],
+                         "layer_hbm_frac": c["layer_hbm_frac"], "layer_int8_mfma_frac": c["layer_int8_mfma_frac"],
+                         "distinct_experts_per_layer": c["distinct_experts_per_layer"],
+                         "roofline": r["roofline"], "cpu_baseline": r["cpu_baseline"]}
+            for key in ("distinct_experts_min_max", "per_token"):
+                if key in c:
+                    sec[name][key] = c[key]
         line["secondary"] = sec
     print(json.dumps(line), flush=True)
     return 0
 
 
-def run_config(args, name, cfg, steps, warmup, cpu, layers=None):
+def run_config(args, name, cfg, steps, warmup, cpu, layers=None, cpu_seconds=None):
     """One configuration: synthetic weights and inputs in HBM, `steps` timed steps (graph replays unless --eager), the
     dominant launch timed alone, and (cpu) the reference CPU path on this host."""
     import torch
@@ -295,8 +309,10 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None):
     achieved_gbs = dom_bytes / dom_s / 1e9
     achieved_tops = dom_ops / dom_s / 1e12
     if prefill and name == "prefill_long":
-        roof = {"bound": "mfma", "achieved": round(achieved_tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s (int8)",
-                "frac": round(achieved_tops / INT8_PEAK_TOPS, 4)}
+        # the products are f16 MFMAs on exact integer codes (2 flops per multiply-add, as an int8 op count), so the
+        # roofline is the f16 MFMA peak; the fraction of the int8 peak is reported beside it
+        roof = {"bound": "mfma", "achieved": round(achieved_tops, 2), "peak": F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s (f16 MFMA on exact integer codes)", "frac": round(achieved_tops / F16_PEAK_TFLOPS, 4)}
     else:
         roof = {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved_gbs / HBM_PEAK_GBS, 4)}
@@ -306,10 +322,18 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None):
                  "traffic_over_algorithmic": round(traffic / dom_bytes, 3) if traffic else None,
                  "hbm_frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
                  "int8_mfma_frac": round(achieved_tops / INT8_PEAK_TOPS, 4)})
+    if prefill:
+        roof["f16_mfma_frac"] = round(achieved_tops / F16_PEAK_TFLOPS, 4)
+
+    # the verify step: the same tokens through the one-token layer, one token at a time, beside the grouped call
+    per_token = None
+    if name == "verify":
+        per_token = one_token_layers(args, Ws, k, T, N, layers, x0_d, logits_d, sg_d, shared, steps, dev, ms_step)
 
     cpu_res = None
     if cpu:
-        cpu_res = cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared)
+        cpu_res = cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared,
+                               seconds=cpu_seconds)
     config = {
         "workload": f"{name}: {cfg['desc']}",
         "tokens": T, "layers": layers, "hidden": N, "expert_ff": FF, "experts": E, "top_k": k,
@@ -321,13 +345,60 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None):
         "layer_int8_mfma_frac": round(layer_ops / layer_s / 1e12 / INT8_PEAK_TOPS, 5),
         "layer_bytes": int(np.mean(layer_bytes)),
         "distinct_experts_per_layer": float(np.mean(distinct_per_layer)),
+        "distinct_experts_min_max": [int(np.min(distinct_per_layer)), int(np.max(distinct_per_layer))],
         "layer_int8_ops": layer_ops,
     }
+    if per_token is not None:
+        config["per_token"] = per_token
     del mls, Ws, graph, dom_graph
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return {"value": round(value, 2), "ms_per_step": round(ms_step, 4), "config": config, "roofline": roof,
             "cpu_baseline": cpu_res}
+
+
+def one_token_layers(args, Ws, k, T, N, layers, x0_d, logits_d, sg_d, shared, steps, dev, grouped_ms):
+    """The verify step's T tokens through the one-token decode layer one at a time (T launches of the one-token layer
+    per layer, each token's row its own x), timed like the grouped step: what the grouped several-token call saves."""
+    import torch
+
+    from tinystrata_amd import moe
+
+    mls1 = [[moe.MoELayer(Ws[l], k, 1, dev) for _ in range(T)] for l in range(layers)]
+    x1 = torch.empty((T, N), device=dev)
+
+    def step1():
+        x1.copy_(x0_d)
+        for l in range(layers):
+            for t in range(T):
+                row = x1[t:t + 1]
+                mls1[l][t](row, logits_d[l, t:t + 1], sg_d[l, t:t + 1] if shared else None, row)
+
+    step1()
+    torch.cuda.synchronize()
+    graph = None
+    if not args.eager:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step1()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step1()
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay() if graph is not None else step1()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    del mls1, graph
+    return {"what": f"the same {T} tokens through the one-token layer, one launch pair per token and layer",
+            "layer_us": round(ms / layers * 1e3, 3), "ms_per_step": round(ms, 4),
+            "grouped_over_per_token": round(grouped_ms / ms, 4)}
 
 
 def run_hybrid(args, cfg) -> int:
@@ -442,7 +513,7 @@ def cpu_topology():
             "mask_logical": len(mask), "mask_physical": len(cores), "cores": cores}
 
 
-def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared):
+def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layers, T, k, shared, seconds=None):
     """The reference CPU path (its own AVX-512/AVX2 expert rows, oracle/_ref: Q8_K activations) on this host, one
     pinned worker per physical core of the process's CPU mask (at most the GPU's host share), over the same routing
     and weights (each layer's used experts at distinct host addresses), timed for about cpu_seconds.  The reference's
@@ -450,6 +521,7 @@ def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layer
     64 tokens)."""
     import oracle as O
 
+    seconds = args.cpu_seconds if seconds is None else seconds
     topo = cpu_topology()
     threads = max(1, min(CPU_SHARE, topo["mask_physical"]))
     cpus = np.asarray(topo["cores"][:threads], np.int32)
@@ -462,7 +534,7 @@ def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layer
             used = np.unique(ids_host[l][:Tc])
             blobs = [pool[orders[l][e]] for e in used] + ([pool[shared_idx[l]]] if shared else [])
             per.append((np.stack(blobs), None))
-        return cpu_port(L, per, Tc, k, shared, args.cpu_seconds)
+        return cpu_port(L, per, Tc, k, shared, seconds)
     R = O.ref()
     wts_all = [ml.wts.cpu().numpy() for ml in mls]
     runs = []
@@ -500,7 +572,7 @@ def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layer
         return tot  # seconds per pass over every piece, each the median of its iterations
 
     first = one_pass(2)
-    iters = int(max(3, min(5000, args.cpu_seconds / max(first, 1e-6))))
+    iters = int(max(3, min(5000, seconds / max(first, 1e-6))))
     sec = one_pass(iters)
     toks = sum(r[0] for r in runs) * layers
     nbytes = sum(r[7] for r in runs)
@@ -517,7 +589,7 @@ def cpu_baseline(args, L, pool, orders, shared_idx, ids_host, mls, x0, sg, layer
                              if topo["mask_physical"] > CPU_SHARE else
                              "one worker per physical core of the process mask, pinned, the caller working too"),
             "sample": f"{iters} passes x {layers} layers over {len(runs)} piece(s) of {Tc} token(s), median pass; "
-                      f"reference CPU expert rows, Q8_K activations"
+                      f"reference CPU expert rows, " + ("Q8_0" if L.gu_type == 8 else "Q8_K") + " activations"
                       + (f" (the first {sum(r[0] for r in runs)} of the {T}-token chunk)" if T > Tc else "")}
 
 
