@@ -675,6 +675,62 @@ __device__ __forceinline__ void route_select_v(const float (&lv)[kRouteV], int k
         wts[lane] = my_p * inv;
     }
 }
+// route_select_v's rounds with each pick published as it is found: lane 0 stores pick r + 1 into pub[r] (LDS words
+// that start at 0, so a reader polls for a nonzero word) with a relaxed workgroup-scope atomic store, which is a plain
+// ds_write (a volatile store through a generic pointer became a system-coherent flat store and a wait for it, a memory
+// round trip in every round), and after round 0 the whole wave calls after0().  ids / wts as route_select_v, written
+// at the end.
+template <int V, typename After0>
+__device__ __forceinline__ void route_publish_v(const float (&lv)[kRouteV], int k, int lane, int32_t* pub,
+                                                int32_t* ids, float* wts, After0 after0) {
+    uint32_t key[V], id[V];
+    route_prep_v<V>(lv, lane, key, id);
+    float sel_sum = 0.f, my_p = 0.f;
+    int my_id = 0;
+    for (int r = 0; r < k; ++r) {
+        const uint32_t wm = wave_max_u32(key[0]);
+        const uint64_t hit = __ballot(key[0] == wm);
+        int x;
+        if (__builtin_popcountll(hit) == 1)
+            x = __builtin_amdgcn_readlane((int) id[0], (int) __builtin_ctzll(hit));
+        else
+            x = (int) wave_min_u32(key[0] == wm ? id[0] : 0xFFFFFFFFu);
+        if (lane == 0) __hip_atomic_store(pub + r, x + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const bool win = lane == (x & 63);
+#pragma unroll
+        for (int i = 0; i + 1 < V; ++i) {
+            key[i] = win ? key[i + 1] : key[i];
+            id[i] = win ? id[i + 1] : id[i];
+        }
+        key[V - 1] = win ? 0u : key[V - 1];
+        const float p = key_value(wm);
+        sel_sum += p;
+        if (lane == r) {
+            my_id = x;
+            my_p = p;
+        }
+        if (r == 0) after0();
+    }
+    const float inv = 1.0f / __builtin_fmaxf(sel_sum, 6.103515625e-5f);
+    if (lane < k) {
+        ids[lane] = my_id;
+        wts[lane] = my_p * inv;
+    }
+}
+template <typename After0>
+__device__ __forceinline__ void route_publish(const float (&v)[kRouteV], int n_expert, int k, int lane, int32_t* pub,
+                                              int32_t* ids, float* wts, After0 after0) {
+    switch (n_expert / 64) {
+        case 1: route_publish_v<1>(v, k, lane, pub, ids, wts, after0); break;
+        case 2: route_publish_v<2>(v, k, lane, pub, ids, wts, after0); break;
+        case 3: route_publish_v<3>(v, k, lane, pub, ids, wts, after0); break;
+        case 4: route_publish_v<4>(v, k, lane, pub, ids, wts, after0); break;
+        case 5: route_publish_v<5>(v, k, lane, pub, ids, wts, after0); break;
+        case 6: route_publish_v<6>(v, k, lane, pub, ids, wts, after0); break;
+        case 7: route_publish_v<7>(v, k, lane, pub, ids, wts, after0); break;
+        default: route_publish_v<8>(v, k, lane, pub, ids, wts, after0); break;
+    }
+}
 __device__ __forceinline__ void route_select(const float (&v)[kRouteV], int n_expert, int k, int lane, int32_t* ids,
                                              float* wts) {
     switch (n_expert / 64) {

@@ -99,6 +99,8 @@ struct LayerArgs {
     float* hf;                    // one-token launch A: h in fp32 [P][n_ff] (where hc would be); launch B quantizes it
     int h_fp32;                   // launch B reads hf instead of hc / hd
     int rows_w;                   // one-token launch A: rows per wave (the slab holds rows_w rows of each wave)
+    int s1_ppb;                   // slot-by-slot launch A: row pairs of every slot per block (n_ff / grid)
+    int s1_wave[16];              // its waves: slot | first row << 8 | end row << 16 (rows of the slot's 2 ppb)
 };
 
 // one Q8_1 activation unit (32 codes + scale) from LDS planes (codes row-major, one float scale per 32)
@@ -406,7 +408,10 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1_kernel(LayerArgs a) {
     const int sh = a.shared ? 1 : 0;
     const int P = (k + sh) * FF;  // row pairs: [shared | pick 0 | ... | pick k-1]
     const int nb = (int) gridDim.x, b = (int) blockIdx.x;
-    const int p0 = (int) ((int64_t) b * P / nb), p1 = (int) ((int64_t) (b + 1) * P / nb);
+    // 32-bit: every wave of the block runs this, and a 64-bit division is a long scalar sequence that the CU's
+    // one scalar unit would serialize over the 16 waves
+    const int p0 = (int) ((uint32_t) b * (uint32_t) P / (uint32_t) nb),
+              p1 = (int) ((uint32_t) (b + 1) * (uint32_t) P / (uint32_t) nb);
     const int nrows = 2 * (p1 - p0);
     const int rounds = max(0, (p1 - 1) / FF + 1 - sh);  // the picks this block's pairs reach
 
@@ -538,6 +543,210 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1_kernel(LayerArgs a) {
         const int pos = slot < sh ? k : slot - sh;
         const float gt = s_row[2 * i];
         a.hf[(int64_t) pos * FF + r] = (gt / (1.0f + expf(-gt))) * s_row[2 * i + 1];
+    }
+}
+
+// ------------------------------------------------------------------ launch A at one token, slot by slot
+// The one-token launch above gives each block a run of consecutive row pairs, so the blocks of the last pick wait for
+// all k rounds of the top-k before they can request a row, and the launch ends with them.  Here every block takes the
+// same pairs [q0, q1) = [n_ff b / nb, n_ff (b + 1) / nb) of EVERY slot (slot 0 the shared expert when there is one,
+// then picks 0 .. k-1): the blocks have equal work and equal routing, and within a block each slot's waves request
+// their rows as soon as the routing wave (wave 0) has published that slot's pick in LDS, so the early picks' rows are
+// in flight, and then dotted, while the later rounds still run; the shared expert's rows are requested at once.
+// Waves are dealt to the slots from the last slot backwards (the routing wave first, to the last pick, whose id it
+// knows first), as evenly as 16 waves allow; a slot's rows (gate and up of each pair, in pair order) are split over
+// its waves (the host's table, s1_wave).  Waves 1-15 quantize x into LDS and store the codebook copies while wave 0
+// routes, and count themselves in an LDS word that every wave reads before its first dot: the block meets only at
+// the start (before anything waits for memory) and at the end, so no wave idles at a barrier while the routing runs.
+// Launch B is unchanged: it reads h in fp32 and the tables block 0 writes.
+constexpr int kRowsS1 = 64;  // rows of a block: slots x 2 pairs per slot, at most
+template <int GT>
+__global__ void __launch_bounds__(kThreadsA) layer_gu1s_kernel(LayerArgs a) {
+#pragma clang fp contract(off)
+    constexpr int kHelp = kThreadsA - 64;  // the threads of waves 1-15
+    constexpr int RPH = (rep_stores<GT>() + kHelp - 1) / kHelp;
+    using Tab = std::conditional_t<(RPH > 0), RepTab<GT>, GridRef>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int32_t s_pub[16];  // pick j + 1 once wave 0 has found it (0 before)
+    __shared__ int32_t s_ready;    // helper waves whose x planes and codebook copies are in LDS
+    __shared__ int32_t s_ids[16];
+    __shared__ float s_pw[16];
+    __shared__ float s_row[kRowsS1];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int k = a.k;
+    const tsx_expert_layout L = a.L;
+    const int N = (int) L.n_embd, NU = N / 32, FF = (int) L.n_ff;
+    const int sh = a.shared ? 1 : 0, S = k + sh;
+    const int b = (int) blockIdx.x;
+    // no division here: every wave runs this prologue, and the CU's one scalar unit would serialize a division's
+    // long scalar sequence over the 16 waves (a 64-bit one held the last wave ~1.3 us)
+    const int q0 = b * a.s1_ppb, q1 = q0 + a.s1_ppb;
+    const int rs = 2 * a.s1_ppb;  // rows of each slot in this block
+    // this wave's slot and its rows of the slot (the host's table: tsx_moe_decode_layer)
+    const int wm = a.s1_wave[wave];
+    const int slot = wm & 255, j0 = (wm >> 8) & 255, j1 = wm >> 16;
+    const int my_rows = j1 - j0;
+
+    if (tid < 16) s_pub[tid] = 0;
+    if (tid == 16) s_ready = 0;
+    // 0. requested first: wave 0 the logits, waves 1-15 the codebooks and the activations
+    float lg[kRouteV];
+    if (wave == 0) route_fetch(a.logits, a.n_expert, lane, lg);
+    uint64_t rv[RPH > 0 ? RPH : 1];
+    if constexpr (RPH > 0)
+        if (wave > 0) rep_fetch<GT, RPH>(rv, tid - 64, kHelp);
+    const int nq_all = N / 4, xt = tid - 64, nxt = kHelp;
+    const float4* x4 = (const float4*) a.x;
+    float4 xv[kXLoads];
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(max(xt, 0) + nxt * i, nq_all - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    // the words above are set before any wave polls them: the block meets once here, while the loads are in flight
+    // (nothing waits for them yet, and every wave of the block has started within ~0.1 us)
+    __syncthreads();
+    const uint64_t gu_row = L.gu_row;
+    const int ppr = (int) (gu_row / 16), cpr = (ppr + 63) / 64;
+    v4i* wslab = (v4i*) smem + wave * (a.rows_w * ppr);
+    uint8_t* tabs = smem + (size_t) kWavesA * a.rows_w * gu_row;
+    int8_t* s_xq = (int8_t*) (tabs + rep_lds_bytes<GT>());
+    float* s_xd = (float*) (s_xq + N);
+
+    // a wave's rows: j0 + j of its slot, pair q0 + (j0 + j) / 2, gate rows for even, up rows for odd (the address is
+    // the same in every lane); issued into registers, then into the wave's slab, dotted with x, reduced over the wave
+    auto rows = [&](auto RC, auto& reg, const uint8_t* blob) {
+        constexpr int R = decltype(RC)::value;
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const int jj = j0 + j;
+            const gbl_ptr<const v4i> src =
+                gbl_at<v4i>((uintptr_t) (blob + ((jj & 1) ? L.up_off : 0) + (uint64_t) (q0 + jj / 2) * gu_row));
+#pragma unroll
+            for (int c = 0; c < kPiecesRow1; ++c)
+                if (c < cpr) reg[j][c] = __builtin_nontemporal_load(src + min(lane + 64 * c, ppr - 1));
+        }
+    };
+    auto dots = [&](auto RC, auto& reg, const Tab& grid) {
+        constexpr int R = decltype(RC)::value;
+        // x and the codebooks: every helper wave has counted itself in s_ready after its LDS stores
+        while (__hip_atomic_load(&s_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kWavesA - 1)
+            __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+#pragma unroll
+            for (int c = 0; c < kPiecesRow1; ++c)
+                if (c < cpr && lane + 64 * c < ppr) wslab[j * ppr + lane + 64 * c] = reg[j][c];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's LDS writes land before its reads
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        float acc[R] = {};
+        for (int u = lane; u < NU; u += 64) {
+            Act xa;
+            act_planes(s_xq + 32 * u, s_xd + u, xa);
+            Unit w[R];
+#pragma unroll
+            for (int j = 0; j < R; ++j) unit_load<GT>((const uint8_t*) (wslab + j * ppr), u, w[j], grid);
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                int Sx, Mx;
+                acc[j] += unit_dot<GT>(w[j], xa, Sx, Mx);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            const float v = lanes_sum<64>(acc[j]);
+            if (lane == 0) s_row[slot * rs + j0 + j] = v;
+        }
+    };
+    // the slot's pick, polled in LDS until wave 0 has published it (relaxed atomic loads: a fresh ds_read every time
+    // round)
+    auto pick_blob = [&]() -> const uint8_t* {
+        if (sh && slot == 0) return a.shared;
+        int id1;
+        while ((id1 = __hip_atomic_load(s_pub + slot - sh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0)
+            __builtin_amdgcn_s_sleep(1);
+        return a.blobs + (uint64_t) (id1 - 1) * a.stride;
+    };
+    // per row count (the same in every lane of a wave) as straight-line code
+    auto with_rows = [&](auto fn) {
+        switch (my_rows) {
+            case 0: fn(std::integral_constant<int, 0>{}); break;
+            case 1: fn(std::integral_constant<int, 1>{}); break;
+            case 2: fn(std::integral_constant<int, 2>{}); break;
+            case 3: fn(std::integral_constant<int, 3>{}); break;
+            default: fn(std::integral_constant<int, 4>{}); break;
+        }
+    };
+
+    if (wave == 0) {
+        // 1. the routing, then this wave's rows of the last pick; at raised issue priority, for the other waves
+        //    dot the early picks' rows on the same SIMD meanwhile
+        __builtin_amdgcn_s_setprio(2);
+        route_publish(lg, a.n_expert, k, lane, s_pub, s_ids, s_pw, [] {});
+        __builtin_amdgcn_s_setprio(0);
+        Tab grid;
+        if constexpr (RPH > 0) grid = rep_view<GT>(tabs);
+        else grid = grid_const();
+        with_rows([&](auto RC) {
+            constexpr int R = decltype(RC)::value;
+            if constexpr (R > 0) {
+                v4i reg[R][kPiecesRow1];
+                rows(RC, reg, pick_blob());
+                dots(RC, reg, grid);
+            }
+        });
+    } else {
+        // 1. x into Q8_1 LDS planes and the codebook copies, while wave 0 routes (one copy of this code for every
+        //    helper wave, ahead of the per-row-count code)
+        for (int bq = 0; bq < nq_all; bq += nxt * kXLoads) {
+            if (bq > 0) {
+#pragma unroll
+                for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(bq + xt + nxt * i, nq_all - 1)];
+            }
+#pragma unroll
+            for (int i = 0; i < kXLoads; ++i) {
+                const int qd = bq + xt + nxt * i;
+                if (bq + (xt & ~63) + nxt * i < nq_all)  // whole waves: one with no quad of x skips the quantize
+                    q8_1_quad_to_lds(xv[i], qd < nq_all, s_xq + 4 * qd, s_xd + qd / 8, xt & 7);
+            }
+        }
+        Tab grid;
+        if constexpr (RPH > 0) grid = rep_store<GT, RPH>(tabs, rv, tid - 64, kHelp);
+        else grid = grid_const();
+        // this wave's LDS stores are done: count it in (read by every wave before its first dot)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if (lane == 0) __hip_atomic_fetch_add(&s_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        with_rows([&](auto RC) {
+            constexpr int R = decltype(RC)::value;
+            v4i reg[R > 0 ? R : 1][kPiecesRow1];
+            // 2. the rows (the shared expert's at once, a routed slot's once its pick is out), their dots; the row
+            //    loads come after the stores above, for a load issued on one path only would make the waits for x
+            //    and the codebooks wait for it too
+            if constexpr (R > 0) {
+                rows(RC, reg, pick_blob());
+                dots(RC, reg, grid);
+            }
+        });
+    }
+    __syncthreads();  // every row's dot is in s_row; the ids and weights in s_ids / s_pw
+    // 3. h = silu(gate) * up per pair (the product rounded on its own), in fp32 at its position: pick j -> j,
+    //    shared -> k; block 0 writes the tables launch B reads (group g = pick g, entry g, position g)
+    for (int i = tid; i < S * (q1 - q0); i += kThreadsA) {
+        const int s = i / (q1 - q0), pr = q0 + i % (q1 - q0);
+        const int pos = s < sh ? k : s - sh;
+        const float gt = s_row[s * rs + 2 * (pr - q0)];
+        a.hf[(int64_t) pos * FF + pr] = (gt / (1.0f + expf(-gt))) * s_row[s * rs + 2 * (pr - q0) + 1];
+    }
+    if (b == 0) {
+        if (tid < k) {
+            a.ids[tid] = s_ids[tid];
+            a.wts[tid] = s_pw[tid];
+            a.tab->wts[tid] = s_pw[tid];
+            a.tab->ent_pos[tid] = tid;
+            a.tab->grp_expert[tid] = s_ids[tid];
+        }
+        if (tid <= k) a.tab->grp_start[tid] = tid;
+        if (tid == 0) a.tab->n_groups = k;
     }
 }
 
@@ -928,7 +1137,7 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
                 "tsx_moe_decode_layer: blobs, stride, shared and x 16-byte aligned, scratch 256-byte aligned");
     TSX_REQUIRE(!norm_w || (h && aligned(h, 4) && (!hq || aligned(hq, 2)) && L.n_embd % 32 == 0),
                 "tsx_moe_decode_layer_norm: h (4-byte aligned) with norm_w; hq 2-byte aligned");
-    LayerArgs a;
+    LayerArgs a{};
     a.L = L;
     a.blobs = (const uint8_t*) blobs;
     a.stride = stride;
@@ -958,6 +1167,48 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
     // one token: the row pairs spread over every CU (launch B quantizes the fp32 h) when the rows tile the slab
     int rc = TSX_ERR_UNSUPPORTED;
     if (n_tok == 1 && L.gu_row % 16 == 0) {
+        // slot by slot where 16 waves can take every slot's rows, at most kMaxRowsW1 per wave, and the grid divides
+        // n_ff: waves are dealt to slots S-1, S-2, ... in turn, base of them each and one more for the last extra
+        // slots, and a slot's rows split evenly over its waves
+        const int S = k + (shared ? 1 : 0), nb = std::min(kBlocksA, (int) L.n_ff);
+        const int ppb = (int) L.n_ff / nb, rs = 2 * ppb, per = S <= kWavesA ? kWavesA / S : 0;
+        const int rows_w = per > 0 && L.n_ff % nb == 0 ? (rs + per - 1) / per : INT_MAX;
+        if (rows_w <= kMaxRowsW1) {
+            // the waves in this order: those of wave 0's SIMD first (waves 4 j share a SIMD), so that the latest picks
+            // go to them and they wait, rather than dot, while wave 0 routes
+            int order[kWavesA], n = 0;
+            for (int w = 0; w < kWavesA; w += 4) order[n++] = w;
+            for (int w = 0; w < kWavesA; ++w)
+                if (w % 4) order[n++] = w;
+            const int extra = kWavesA % S;
+            int w = 0;
+            for (int slot = S - 1; slot >= 0; --slot) {
+                const int ws = per + (slot >= S - extra ? 1 : 0);
+                for (int iw = 0; iw < ws; ++iw, ++w)
+                    a.s1_wave[order[w]] = slot | (rs * iw / ws) << 8 | (rs * (iw + 1) / ws) << 16;
+            }
+            a.s1_ppb = ppb;
+        }
+        size_t lim1 = 0;
+        with_type(L.gu_type, [&](auto T) {
+            static const size_t limit = set_max_lds((const void*) layer_gu1s_kernel<decltype(T)::value>);
+            lim1 = limit;
+            return 0;
+        });
+        const size_t lds1 = rows_w <= kMaxRowsW1 ? (size_t) kWavesA * rows_w * L.gu_row + rep_bytes(L.gu_type) +
+                                                       x_planes_bytes(L, 1)
+                                                 : SIZE_MAX;
+        if (rows_w <= kMaxRowsW1 && S * rs <= kRowsS1 && L.gu_row <= (uint64_t) 64 * kPiecesRow1 * 16 &&
+            lds1 <= lim1) {
+            a.h_fp32 = 1;
+            a.rows_w = rows_w;
+            rc = with_type(L.gu_type, [&](auto T) {
+                layer_gu1s_kernel<decltype(T)::value><<<nb, kThreadsA, lds1, s>>>(a);
+                return launch_status("tsx_moe_decode_layer/gate-up");
+            });
+        }
+    }
+    if (n_tok == 1 && L.gu_row % 16 == 0 && !a.h_fp32) {
         const int pairs = (k + (shared ? 1 : 0)) * (int) L.n_ff, nb = std::min(kBlocksA, pairs);
         const int rows = 2 * ((pairs + nb - 1) / nb), rows_w = (rows + kWavesA - 1) / kWavesA;
         size_t lim1 = 0;
