@@ -377,7 +377,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                                                           const int32_t* __restrict__ bounds,
                                                           const int32_t* __restrict__ ids, float* __restrict__ dst,
                                                           int64_t ld_dst, const int32_t* __restrict__ xids = nullptr,
-                                                          MmqPlanes H = MmqPlanes{}, int n_ff = 0) {
+                                                          MmqPlanes H = MmqPlanes{}, int n_ff = 0, int tpg = 0) {
     constexpr int NT = 64 * NW, BM = 32 * NW, NB = f16_buffers<T, NW>(), kBN = bn_of<T>();
     constexpr int CB = chunk_bytes<T>(), RS = raw_stride<T>(), PR = RS / 16, RW = (32 * PR + 63) / 64;
     constexpr int BP = kBN * 16 / NT, EPT = kMaxExpertsMmq / NT;
@@ -409,7 +409,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     auto& tB = *reinterpret_cast<_Float16(*)[NB][kBN * kBStride]>(s_lds + L::TB);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int bx = blockIdx.x, by = blockIdx.y;
+    // Which (column block bx, token tile by): workgroups go to the 8 XCDs in turn by their linear index, so with
+    // tpg > 0 the s-th block to reach XCD x takes item ((s / G) * 8 + x) * G + s % G of the (tile-major) items,
+    // G = gridDim.x * tpg: runs of tpg consecutive tiles, all their column blocks, share an XCD and its L2 (a tile's
+    // activation rows serve every column block, and an expert's weights its next tiles), while the runs still come in
+    // tile order over the whole chip.  The host pads gridDim.y to a multiple of 8 tpg (a bijection on the grid).
+    int bx = blockIdx.x, by = blockIdx.y;
+    if (tpg > 0) {
+        const int nbx = (int) gridDim.x, lin = bx + nbx * by, G = nbx * tpg;
+        const int xcd = lin & 7, sx = lin >> 3;
+        const int item = ((sx / G) * 8 + xcd) * G + sx % G;
+        bx = item % nbx;
+        by = item / nbx;
+    }
     const int lr = lane & 15, g = lane >> 4;
 
     // 1. which expert and which of its token tiles: EPT experts per thread, a block scan of tile counts.  The full
@@ -1049,6 +1061,12 @@ TSX_API int tsx_moe_mmq_quantize_route(const float* x, void* xq, int type, int64
     return launch_status("tsx_moe_mmq_quantize_route");
 }
 
+// runs of kXcdTiles consecutive token tiles per XCD (mmq_f16_kernel's tpg); the tile grid padded to whole rounds of
+// runs over the 8 XCDs, its extra blocks returning at once like the tiles past the routing's count
+// (2 measured best of 0, 1, 2, 4, 8: configs[3] gate/up 168 -> 162 us, configs[4] 345.5 -> 343 us; 8 lost 10 %)
+constexpr int kXcdTiles = 2;
+inline int64_t xcd_tiles(int64_t tiles) { return (tiles + 8 * kXcdTiles - 1) / (8 * kXcdTiles) * (8 * kXcdTiles); }
+
 TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
     TSX_REQUIRE(p != nullptr, "tsx_moe_mmq_run: null product");
     const size_t rb = tsx_row_bytes(p->type, p->w_cols);
@@ -1068,21 +1086,22 @@ TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
         const int nw = p->type == TSX_Q4_K && p->w_rows % 128 == 0 ? 4 : p->w_rows % 256 == 0 ? 8 : p->w_rows % 128 == 0 ? 4 : 2;
         return with_type(p->type, [&](auto T) {
             constexpr int TT = decltype(T)::value;
-            const int64_t max_tiles = (p->total_rows + bn_of<TT>() - 1) / bn_of<TT>() + p->n;
+            const int64_t max_tiles = xcd_tiles((p->total_rows + bn_of<TT>() - 1) / bn_of<TT>() + p->n);
             const dim3 grid((unsigned) (p->w_rows / (32 * nw)), (unsigned) max_tiles);
             const uint8_t* w = (const uint8_t*) p->w;
             if (nw == 8 && p->w_cols <= kPassCols && p->w_rows % 512 == 0)
                 mmq_f16_kernel<TT, 8, false, 2><<<dim3(grid.x / 2, grid.y), 512, 0, s>>>(
-                    w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds, p->ids, p->dst, p->ld_dst);
+                    w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds, p->ids, p->dst, p->ld_dst, nullptr,
+                    MmqPlanes{}, 0, kXcdTiles);
             else if (nw == 8)
                 mmq_f16_kernel<TT, 8><<<grid, 512, 0, s>>>(w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds,
-                                                           p->ids, p->dst, p->ld_dst);
+                                                           p->ids, p->dst, p->ld_dst, nullptr, MmqPlanes{}, 0, kXcdTiles);
             else if (nw == 4)
                 mmq_f16_kernel<TT, 4><<<grid, 256, 0, s>>>(w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds,
-                                                           p->ids, p->dst, p->ld_dst);
+                                                           p->ids, p->dst, p->ld_dst, nullptr, MmqPlanes{}, 0, kXcdTiles);
             else
                 mmq_f16_kernel<TT, 2><<<grid, 128, 0, s>>>(w, p->expert_bytes, rb, (int) p->w_cols, p->n, P, p->bounds,
-                                                           p->ids, p->dst, p->ld_dst);
+                                                           p->ids, p->dst, p->ld_dst, nullptr, MmqPlanes{}, 0, kXcdTiles);
             return launch_status("tsx_moe_mmq_run/mfma");
         });
     }
@@ -1119,11 +1138,12 @@ TSX_API int tsx_moe_mmq_gate_up_swiglu(const void* w, int type, int64_t n_ff, in
     const hipStream_t s = (hipStream_t) stream;
     return with_type(type, [&](auto T) {
         constexpr int BN = bn_of<decltype(T)::value>();
-        const int64_t max_tiles = (n_rows + BN - 1) / BN + n_exp;
+        const int64_t max_tiles = xcd_tiles((n_rows + BN - 1) / BN + n_exp);
         constexpr int NW = nw_of<decltype(T)::value>();
         const dim3 grid((unsigned) (n_ff / (16 * NW)), (unsigned) max_tiles);
         mmq_f16_kernel<decltype(T)::value, NW, true><<<grid, 64 * NW, 0, s>>>(
-            (const uint8_t*) w, expert_bytes, rb, (int) n_embd, n_exp, P, bounds, nullptr, nullptr, 0, xids, H, (int) n_ff);
+            (const uint8_t*) w, expert_bytes, rb, (int) n_embd, n_exp, P, bounds, nullptr, nullptr, 0, xids, H, (int) n_ff,
+            kXcdTiles);
         return launch_status("tsx_moe_mmq_gate_up_swiglu");
     });
 }
