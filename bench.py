@@ -82,17 +82,38 @@ def parse_args(argv=None):
                     help="end every layer with the MoE block's norm epilogue (h = rms(x) * norm_w and its Q8_1 image)")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the prompt-chunk configurations measured after the default decode line")
+    ap.add_argument("--layers", type=int, default=0,
+                    help="layers per step (default: the configuration's; the default line's prompt-chunk entries use 2)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--secondary-cpu-seconds", type=float, default=4.0,
                     help="CPU baseline sample of each secondary configuration")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="before the timed region, run one plain fp32 copy kernel (out = in * 1) over this many MiB: "
                          "the known-size launch that scales rocprofv3's FETCH_SIZE / WRITE_SIZE to bytes")
+    ap.add_argument("--trace-marks", action="store_true",
+                    help="launch a tiny int16 fill just before and just after the timed steps, and an int8 fill "
+                         "around the dominant-launch loop, outside both timed regions, so that --summarize-trace can "
+                         "pick those regions' dispatches out of a rocprofv3 kernel trace")
+    ap.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                    help="no GPU work: summarize a rocprofv3 kernel trace of a --trace-marks run (the dispatches "
+                         "between the marks only) as markdown")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="no GPU work: HBM bytes per dominant launch from two rocprofv3 --pmc counter files "
+                         "(FETCH_SIZE, WRITE_SIZE) of a --copy-probe-mib run; prints markdown and, with "
+                         "--traffic-json, records the figure under --config's name")
+    ap.add_argument("--traffic-json", help="with --summarize-pmc: the traffic record to update (profiles/traffic.json)")
+    ap.add_argument("--pmc-source", default="", help="with --summarize-pmc: the commands that made the counter files")
     return ap.parse_args(argv)
 
 
 def main() -> int:
     args = parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace, args.steps))
+        return 0
+    if args.summarize_pmc:
+        print(summarize_pmc(args, *args.summarize_pmc))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU; --gpus N > 1 is not supported (the sharding plan is design only)",
               file=sys.stderr)
@@ -100,7 +121,7 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     if "resident" in cfg:
         return run_hybrid(args, cfg)
-    res = run_config(args, args.config, cfg, args.steps, args.warmup, cpu=not args.no_cpu)
+    res = run_config(args, args.config, cfg, args.steps, args.warmup, cpu=not args.no_cpu, layers=args.layers or None)
     line = {
         "metric": METRIC,
         "value": res["value"],
@@ -227,11 +248,14 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None, cpu_seconds=Non
 
     # ---------------------------------------------------------------- timed region
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    mark = (lambda dt: torch.full((3,), 7, dtype=dt, device=dev)) if args.trace_marks else (lambda dt: None)
     torch.cuda.synchronize()
+    mark(torch.int16)
     start.record()
     for _ in range(steps):
         graph.replay() if graph is not None else step()
     end.record()
+    mark(torch.int16)
     torch.cuda.synchronize()
     ms_step = start.elapsed_time(end) / steps
     value = layers * T / (ms_step / 1e3)
@@ -300,10 +324,12 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None, cpu_seconds=Non
             dom()
         dom_graph.replay()
     torch.cuda.synchronize()
+    mark(torch.int8)
     ev0.record()
     for _ in range(reps):
         dom_graph.replay() if dom_graph is not None else dom()
     ev1.record()
+    mark(torch.int8)
     torch.cuda.synchronize()
     dom_s = ev0.elapsed_time(ev1) / (reps * layers) / 1e3
     achieved_gbs = dom_bytes / dom_s / 1e9
@@ -466,6 +492,102 @@ def run_hybrid(args, cfg) -> int:
     }))
     cpu.close()
     return 0
+
+
+# ---------------------------------------------------------------- profile summaries (no GPU work)
+MARK_STEP, MARK_DOM = "FillFunctor<short>", "FillFunctor<signed char>"
+
+
+def _short_kernel(name: str) -> str:
+    import re
+
+    m = re.search(r"(\w+_kernel<[^>]*>|\w+_kernel\b|__amd_rocclr_\w+)", name)
+    return m.group(1) if m else name[:60]
+
+
+def summarize_trace(path: str, steps: int) -> str:
+    """Markdown: per kernel and launch shape, the dispatches between each pair of --trace-marks marks (the timed steps,
+    then the dominant-launch loop), with each region's span on the GPU clock."""
+    import csv
+    import statistics
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Start_Timestamp"]))
+    out = []
+    for label, mark in (("timed steps", MARK_STEP), ("dominant-launch loop", MARK_DOM)):
+        at = [i for i, r in enumerate(rows) if mark in r["Kernel_Name"]]
+        if len(at) < 2:
+            out.append(f"{label}: no marks in {path}")
+            continue
+        sel = rows[at[0] + 1: at[1]]
+        span = (int(sel[-1]["End_Timestamp"]) - int(sel[0]["Start_Timestamp"])) / 1e3
+        per = {}
+        for r in sel:
+            g = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+            key = (_short_kernel(r["Kernel_Name"]), g // max(wg, 1), wg)
+            per.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        busy = sum(sum(v) for v in per.values())
+        out.append(f"**{label}**: {len(sel)} dispatches over {span:.1f} us of GPU time (first start to last end)"
+                   + (f", {span / steps:.1f} us per step" if label == "timed steps" else "") + "; kernels busy "
+                   f"{busy:.1f} us")
+        out.append("")
+        out.append("| kernel | blocks x threads | calls | avg us | median us | min us | max us | % of span |")
+        out.append("|---|---|---|---|---|---|---|---|")
+        for k, v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            out.append(f"| {k[0]} | {k[1]} x {k[2]} | {len(v)} | {statistics.mean(v):.2f} | "
+                       f"{statistics.median(v):.2f} | {min(v):.2f} | {max(v):.2f} | {100 * sum(v) / span:.1f} |")
+        out.append("")
+    return "\n".join(out)
+
+
+# the dominant launch of each configuration, as kernel-name fragments (per layer for the decode configurations)
+DOMINANT = {"decode": ("layer_gu1s_kernel", "layer_down_kernel"), "plumb": ("layer_gu1s_kernel", "layer_down_kernel"),
+            "verify": ("layer_gu_kernel", "layer_down_kernel"), "prefill": ("mmq_f16_kernel<12, 4, true",),
+            "prefill_long": ("mmq_f16_kernel<18, 8, true",)}
+
+
+def summarize_pmc(args, fetch_csv: str, write_csv: str) -> str:
+    """HBM bytes per dominant launch: each counter's KiB per dispatch, averaged per kernel, scaled by what the same
+    counter read for the copy probe (--copy-probe-mib: a known number of bytes in and out)."""
+    import csv
+
+    mib = args.copy_probe_mib or 1024
+    vals = {}
+    for ctr, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        per = {}
+        for r in csv.DictReader(open(path)):
+            if r.get("Counter_Name", ctr) != ctr:
+                continue
+            name = r["Kernel_Name"]
+            key = "copy probe" if "elementwise" in name and "Mul" in name else _short_kernel(name)
+            per.setdefault(key, []).append(float(r["Counter_Value"]))
+        vals[ctr] = per
+    probe = {c: max(vals[c].get("copy probe", [0.0])) for c in vals}
+    fac = {c: probe[c] / (mib * 1024.0) for c in probe}  # counter KiB per true KiB
+    lines = [f"copy probe ({mib} MiB in, {mib} MiB out): FETCH_SIZE {probe['FETCH_SIZE']:.1f} KiB, WRITE_SIZE "
+             f"{probe['WRITE_SIZE']:.1f} KiB -> factors {fac['FETCH_SIZE']:.3f} (fetch), {fac['WRITE_SIZE']:.3f} (write)",
+             "", "| kernel | dispatches | FETCH_SIZE KiB / dispatch | WRITE_SIZE KiB / dispatch | bytes / dispatch |",
+             "|---|---|---|---|---|"]
+    dom = DOMINANT.get(args.config, ())
+    total = 0.0
+    for k in sorted(set(vals["FETCH_SIZE"]) | set(vals["WRITE_SIZE"])):
+        if k == "copy probe":
+            continue
+        f, w = vals["FETCH_SIZE"].get(k, [0.0]), vals["WRITE_SIZE"].get(k, [0.0])
+        fa, wa = sum(f) / len(f), sum(w) / len(w)
+        b = (fa / fac["FETCH_SIZE"] + wa / fac["WRITE_SIZE"]) * 1024
+        lines.append(f"| {k} | {len(f)} | {fa:.1f} | {wa:.1f} | {b:,.0f} |")
+        if any(d in k for d in dom):
+            total += b
+    lines += ["", f"dominant launch ({' + '.join(dom)}): {total:,.0f} bytes"]
+    if args.traffic_json:
+        f = Path(args.traffic_json)
+        rec = json.loads(f.read_text()) if f.exists() else {}
+        rec[args.config] = {"hbm_bytes_per_launch": int(round(total)), "launch": " + ".join(dom),
+                            "fetch_factor": round(fac["FETCH_SIZE"], 4), "write_factor": round(fac["WRITE_SIZE"], 4),
+                            "source": args.pmc_source}
+        f.write_text(json.dumps(rec, indent=1) + "\n")
+    return "\n".join(lines)
 
 
 def measured_traffic(config: str):
