@@ -540,10 +540,12 @@ def summarize_trace(path: str, steps: int) -> str:
     return "\n".join(out)
 
 
-# the dominant launch of each configuration, as kernel-name fragments (per layer for the decode configurations)
-DOMINANT = {"decode": ("layer_gu1s_kernel", "layer_down_kernel"), "plumb": ("layer_gu1s_kernel", "layer_down_kernel"),
-            "verify": ("layer_gu_kernel", "layer_down_kernel"), "prefill": ("mmq_f16_kernel<12, 4, true",),
-            "prefill_long": ("mmq_f16_kernel<18, 8, true",)}
+# the dominant launch of each configuration by kernel (per layer for the decode configurations: both launches); where
+# one kernel runs at two grid sizes (the prompt products of the routed and the shared experts) the larger grid's
+DOMINANT = {"decode": ("layer_gu1s_kernel<18>", "layer_down_kernel<21, 1>"),
+            "plumb": ("layer_gu1s_kernel<8>", "layer_down_kernel<8, 4>"),
+            "verify": ("layer_gu_kernel<18>", "layer_down_kernel<21, 4>"),
+            "prefill": ("mmq_f16_kernel<12, 4, true, 1>",), "prefill_long": ("mmq_f16_kernel<18, 8, true, 1>",)}
 
 
 def summarize_pmc(args, fetch_csv: str, write_csv: str) -> str:
@@ -559,26 +561,33 @@ def summarize_pmc(args, fetch_csv: str, write_csv: str) -> str:
             if r.get("Counter_Name", ctr) != ctr:
                 continue
             name = r["Kernel_Name"]
-            key = "copy probe" if "elementwise" in name and "Mul" in name else _short_kernel(name)
+            if "elementwise" in name and "Mul" not in name:
+                continue  # torch's fills of the probe's buffers
+            blocks = int(r["Grid_Size"]) // max(1, int(r["Workgroup_Size"]))
+            key = ("copy probe", 0) if "elementwise" in name else (_short_kernel(name), blocks)
             per.setdefault(key, []).append(float(r["Counter_Value"]))
         vals[ctr] = per
-    probe = {c: max(vals[c].get("copy probe", [0.0])) for c in vals}
+    probe = {c: max(vals[c].get(("copy probe", 0), [0.0])) for c in vals}
     fac = {c: probe[c] / (mib * 1024.0) for c in probe}  # counter KiB per true KiB
     lines = [f"copy probe ({mib} MiB in, {mib} MiB out): FETCH_SIZE {probe['FETCH_SIZE']:.1f} KiB, WRITE_SIZE "
              f"{probe['WRITE_SIZE']:.1f} KiB -> factors {fac['FETCH_SIZE']:.3f} (fetch), {fac['WRITE_SIZE']:.3f} (write)",
-             "", "| kernel | dispatches | FETCH_SIZE KiB / dispatch | WRITE_SIZE KiB / dispatch | bytes / dispatch |",
-             "|---|---|---|---|---|"]
+             "", "| kernel | blocks | dispatches | FETCH_SIZE KiB / dispatch | WRITE_SIZE KiB / dispatch | bytes / dispatch |",
+             "|---|---|---|---|---|---|"]
     dom = DOMINANT.get(args.config, ())
-    total = 0.0
+    per_bytes = {}
     for k in sorted(set(vals["FETCH_SIZE"]) | set(vals["WRITE_SIZE"])):
-        if k == "copy probe":
+        if k[0] == "copy probe":
             continue
         f, w = vals["FETCH_SIZE"].get(k, [0.0]), vals["WRITE_SIZE"].get(k, [0.0])
         fa, wa = sum(f) / len(f), sum(w) / len(w)
         b = (fa / fac["FETCH_SIZE"] + wa / fac["WRITE_SIZE"]) * 1024
-        lines.append(f"| {k} | {len(f)} | {fa:.1f} | {wa:.1f} | {b:,.0f} |")
-        if any(d in k for d in dom):
-            total += b
+        lines.append(f"| {k[0]} | {k[1]} | {len(f)} | {fa:.1f} | {wa:.1f} | {b:,.0f} |")
+        per_bytes[k] = b
+    total = 0.0
+    for d in dom:  # each dominant kernel at its largest grid
+        grids = [k for k in per_bytes if k[0] == d]
+        if grids:
+            total += per_bytes[max(grids, key=lambda k: k[1])]
     lines += ["", f"dominant launch ({' + '.join(dom)}): {total:,.0f} bytes"]
     if args.traffic_json:
         f = Path(args.traffic_json)
