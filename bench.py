@@ -307,7 +307,7 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None, cpu_seconds=Non
                                      ml.lscratch, shared=ml.W.shared, sgate=sg_d[l] if shared else None)
         dom_bytes = float(np.mean(layer_bytes))
         dom_ops = float(layer_ops)
-        kernel = ("tsx_moe_decode_layer (" + ("layer_gu1_kernel" if T == 1 else "layer_gu_kernel") +
+        kernel = ("tsx_moe_decode_layer (" + ("layer_gu1s_kernel" if T == 1 else "layer_gu_kernel") +
                   " + layer_down_kernel) per layer")
     dom()
     torch.cuda.synchronize()
