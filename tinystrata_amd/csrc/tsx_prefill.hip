@@ -463,6 +463,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     auto roff = [&](int r) -> uint64_t {
         return FUSE ? (uint64_t) ((r & 15) + (r >= 16 ? n_ff : 0)) * row_bytes : (uint64_t) r * row_bytes;
     };
+    // where row r's chunk c starts in its slab row: the block's offset within its first 16-byte piece (0 for the
+    // formats whose chunks are whole pieces: the base, expert and row strides are multiples of 16)
+    auto slab_off = [&](int r, int c) -> int {
+        if constexpr (chunk_aligned<T>()) return 0;
+        else return (int) ((roff(r) + (uint64_t) c * CB) & 15);
+    };
     const int nu = w_cols / 32, nchunks = w_cols / kChunk;
     // the activation rows this thread loads (the same every chunk): rows past the tile's last take its last row
     int32_t arow_b[BP];  // row indices (32-bit: widened where the addresses are formed)
@@ -630,15 +636,20 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
             // units 4 hl .. 4 hl + 3); a zero row scale zeroes the row's weights for the chunk
             {
                 const int r = lane & 31, hl = lane >> 5;
-                const uint8_t* b = slab + r * RS + (int) ((roff(r) + (uint64_t) c * CB) & 15);
+                const uint8_t* b = slab + r * RS + slab_off(r, c);
                 const float wold = s_dw[wave][r];
                 if constexpr (T == TSX_IQ3_XXS || IQ3S || Q4K) {
-                    const float d = h2f((uint16_t) ld16(b));
+                    // Q4_K: d and dmin in one aligned word
+                    const uint32_t dd = Q4K ? ld32(b) : ld16(b);
+                    const float d = h2f((uint16_t) dd);
                     const float dw = XXS ? 0.25f * d : d;
                     const float wn = dw != 0.f ? dw : wold;
                     const bool live = dw != 0.f;
+                    // the hardware reciprocal: the ratios only need to chain (the last w' multiplies the result), and
+                    // each is within 2 ulp of the quotient
+                    const float rwn = __builtin_amdgcn_rcpf(wn);
                     if (hl == 0) {
-                        s_rw[wave][r] = wold / wn;
+                        s_rw[wave][r] = wold * rwn;
                         s_dw[wave][r] = wn;
                     }
                     if constexpr (T == TSX_IQ3_XXS) {
@@ -655,21 +666,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                             s_sc[wave][j][r] = live ? hpair(2 * ((b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u) + 1) : 0u;
                         }
                     } else {
-                        const float dmin = h2f((uint16_t) ld16(b + 2)), dr = dmin / wn;
-                        const uint8_t* s12 = b + 4;
+                        const float dmin = h2f((uint16_t) (dd >> 16)), dr = dmin * rwn;
+                        // the 12 scale bytes as three aligned words; sub-blocks 4 hl + k: scale byte k of SC, min
+                        // byte k of M (sub-blocks 0-3: the low 6 bits of bytes 0-3 and 4-7; 4-7: the nibbles of bytes
+                        // 8-11 with the top 2 bits of bytes 0-3 and 4-7 above them)
+                        const uint32_t w0 = ld32(b + 4), w1 = ld32(b + 8), w2 = ld32(b + 12);
+                        const uint32_t SC = hl == 0 ? w0 & 0x3F3F3F3Fu : (w2 & 0x0F0F0F0Fu) | ((w0 >> 2) & 0x30303030u);
+                        const uint32_t M = hl == 0 ? w1 & 0x3F3F3F3Fu
+                                                   : ((w2 >> 4) & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u);
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const int j = 4 * hl + k;
-                            int sc, m;
-                            if (j < 4) {
-                                sc = s12[j] & 63;
-                                m = s12[j + 4] & 63;
-                            } else {
-                                sc = (s12[j + 4] & 15) | ((s12[j - 4] >> 6) << 4);
-                                m = (s12[j + 4] >> 4) | ((s12[j] >> 6) << 4);
-                            }
-                            s_sc[wave][j][r] = live ? hpair((uint32_t) sc) : 0u;
-                            s_uf[wave][j][r] = dr * (float) m;
+                            s_sc[wave][j][r] = live ? hpair((SC >> (8 * k)) & 255u) : 0u;
+                            s_uf[wave][j][r] = dr * (float) ((M >> (8 * k)) & 255u);
                         }
                     }
                 } else {  // Q8_0: a float scale per unit, its ratio applied at every unit
@@ -679,7 +688,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                         for (int j = 0; j < 8; ++j) {
                             const float d = h2f((uint16_t) ld16(b + 34 * j));
                             const float wn = d != 0.f ? d : wv;
-                            s_uf[wave][j][r] = wv / wn;
+                            s_uf[wave][j][r] = wv * __builtin_amdgcn_rcpf(wn);
                             s_sc[wave][j][r] = d != 0.f ? 0x3C003C00u : 0u;
                             wv = wn;
                         }
@@ -693,7 +702,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int r = 16 * t + lr;
-                blk[t] = slab + r * RS + (int) ((roff(r) + (uint64_t) c * CB) & 15);
+                blk[t] = slab + r * RS + slab_off(r, c);
             }
             // unit u's weight fragments (rows 16 t + lr, values 8 g .. 8 g + 7 of the unit), in two halves: raw()
             // reads the unit's indices and scales (the slab and the per-unit arrays), expand() looks the codebooks up
@@ -717,9 +726,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                         R.a[t][1] = b[74 + 4 * u + g];
                         R.a[t][2] = s_sc[wave][u][r];
                     } else if constexpr (Q4K) {
-                        const uint8_t* q = b + 16 + 32 * (u >> 1) + 8 * g;
-                        R.a[t][0] = ld32a2(q);
-                        R.a[t][1] = ld32a2(q + 4);
+                        const uint2 q = *(const uint2*) (b + 16 + 32 * (u >> 1) + 8 * g);  // 8-byte aligned
+                        R.a[t][0] = q.x;
+                        R.a[t][1] = q.y;
                         R.a[t][2] = s_sc[wave][u][r];
                     } else {
                         const uint8_t* q = b + 34 * u + 2 + 8 * g;
