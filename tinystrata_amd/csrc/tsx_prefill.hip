@@ -645,6 +645,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                     const float dw = XXS ? 0.25f * d : d;
                     const float wn = dw != 0.f ? dw : wold;
                     const bool live = dw != 0.f;
+                    const uint32_t keep = 0u - (uint32_t) live;  // a mask: the compiler would branch on live
                     // the hardware reciprocal: the ratios only need to chain (the last w' multiplies the result), and
                     // each is within 2 ulp of the quotient
                     const float rwn = __builtin_amdgcn_rcpf(wn);
@@ -657,27 +658,30 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                         for (int k = 0; k < 4; ++k) {
                             const int j = 4 * hl + k;
                             const uint32_t aux = ld32a2(b + 66 + 4 * j);
-                            s_am[wave][j][r] = uint2{aux, live ? hpair(2 * (aux >> 28) + 1) : 0u};
+                            s_am[wave][j][r] = uint2{aux, hpair(2 * (aux >> 28) + 1) & keep};
                         }
                     } else if constexpr (IQ3S) {
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const int j = 4 * hl + k;
-                            s_sc[wave][j][r] = live ? hpair(2 * ((b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u) + 1) : 0u;
+                            s_sc[wave][j][r] = hpair(2 * ((b[106 + (j >> 1)] >> (4 * (j & 1))) & 15u) + 1) & keep;
                         }
                     } else {
                         const float dmin = h2f((uint16_t) (dd >> 16)), dr = dmin * rwn;
                         // the 12 scale bytes as three aligned words; sub-blocks 4 hl + k: scale byte k of SC, min
                         // byte k of M (sub-blocks 0-3: the low 6 bits of bytes 0-3 and 4-7; 4-7: the nibbles of bytes
                         // 8-11 with the top 2 bits of bytes 0-3 and 4-7 above them)
+                        // (selected with masks: the compiler would otherwise branch on the lane's half)
                         const uint32_t w0 = ld32(b + 4), w1 = ld32(b + 8), w2 = ld32(b + 12);
-                        const uint32_t SC = hl == 0 ? w0 & 0x3F3F3F3Fu : (w2 & 0x0F0F0F0Fu) | ((w0 >> 2) & 0x30303030u);
-                        const uint32_t M = hl == 0 ? w1 & 0x3F3F3F3Fu
-                                                   : ((w2 >> 4) & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u);
+                        const uint32_t lo = 0u - (uint32_t) (hl == 0);
+                        const uint32_t SC = (w0 & 0x3F3F3F3Fu & lo) |
+                                            (((w2 & 0x0F0F0F0Fu) | ((w0 >> 2) & 0x30303030u)) & ~lo);
+                        const uint32_t M = (w1 & 0x3F3F3F3Fu & lo) |
+                                           ((((w2 >> 4) & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u)) & ~lo);
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
                             const int j = 4 * hl + k;
-                            s_sc[wave][j][r] = live ? hpair((SC >> (8 * k)) & 255u) : 0u;
+                            s_sc[wave][j][r] = hpair((SC >> (8 * k)) & 255u) & keep;
                             s_uf[wave][j][r] = dr * (float) ((M >> (8 * k)) & 255u);
                         }
                     }
