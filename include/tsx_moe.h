@@ -132,7 +132,8 @@ TSX_API int tsx_moe_mmvq_slots(int type, const tsx_mmvq_slots* a, int count, int
  * where expert(b, x) = down . Q8_1(silu(gate . Q8_1(x)) * (up . Q8_1(x))) of the blob at b; expert e's blob is at
  * blobs + e * stride.  ids / wts [n_tok][k] receive the routing.  y may alias x.  Limits: n_embd <= 4096,
  * n_ff <= 1024, n_tok * k <= 64, n_expert a multiple of 64 up to 512; blobs, stride and shared 16-byte aligned.
- * scratch: tsx_moe_decode_layer_scratch_bytes(n_tok, k, n_ff) bytes, 256-byte aligned.
+ * scratch: tsx_moe_decode_layer_scratch_bytes(n_tok, k, n_ff) bytes, 256-byte aligned (the tables, and h as Q8_1
+ * planes or, where launch A leaves it in fp32 - one token, or up to four at n_ff <= 512 - as floats).
  * Replaces the MoE block's call sequence at src/qwen35/q36_engine.cu:2821-2925: k_route_group
  * (src/qwen35/q36_kernels.cuh:383-474), native_expert_grouped (src/kernels/cuda/iq_kernels.cu:2835-2982), the shared
  * expert's mmvq / SwiGLU / mmvq (q36_engine.cu:2906-2913) and k_moe_out_small without the norm

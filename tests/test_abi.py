@@ -63,6 +63,21 @@ def test_scratch_bytes_reference_formula():
         assert ops.scratch_hq_offset(cap, ff) == 3 * r(f)
 
 
+def test_decode_layer_scratch_covers_fp32_h():
+    """The decode layer's scratch holds the tables and h as Q8_1 planes, or in fp32 (4 bytes per value, every routed
+    position and every token's shared one) wherever a slot-by-slot launch A may take the call: one token, or up to four
+    tokens at n_ff <= 512.  The multi-token launch A once wrote fp32 h into a scratch sized for the planes."""
+    r = lambda v: (v + 255) // 256 * 256
+    for T, k, ff in [(1, 8, 512), (2, 8, 512), (3, 8, 512), (4, 8, 512), (4, 11, 256), (1, 16, 1024)]:
+        need = (T * k + T) * ff * 4
+        got = ops.decode_layer_scratch_bytes(T, k, ff)
+        assert got >= need + 256, (T, k, ff, got, need)    # the tables come first (at least 256 bytes)
+    for T, k, ff in [(5, 8, 512), (8, 8, 512), (4, 8, 1024), (2, 8, 768)]:
+        planes = (T * k + T) * (ff + ff // 32 * 4)         # codes and a float scale per 32
+        got = ops.decode_layer_scratch_bytes(T, k, ff)
+        assert got >= planes and got < (T * k + T) * ff * 4, (T, k, ff, got)
+
+
 def test_supported_shapes():
     assert ops.native_expert_supported(_lib.IQ3_XXS, _lib.IQ3_S, 2048, 512)
     assert ops.native_expert_supported(_lib.Q4_K, _lib.Q4_K, 2048, 768)

@@ -154,6 +154,11 @@ DECODE_CASES = [
     (Q8_0, Q8_0, 2048, 768, 64, 4, True, 3),          # 8-row chunks
     (IQ3_S, IQ3_XXS, 4096, 256, 512, 2, False, 5),    # widest rows, 512 experts
     (IQ3_XXS, Q8_0, 2048, 1024, 64, 1, True, 1),      # top-1, widest FF
+    # two to four tokens on the slot-by-slot launch A: shared expert items of 2 and 1 rows, no shared expert, rows of
+    # one and of two 16-byte pieces per lane, 2 rows of a slot per block
+    (IQ3_XXS, IQ3_S, 2048, 512, 256, 8, True, 2),
+    (Q4_K, Q4_K, 2048, 512, 128, 8, False, 3),
+    (IQ3_S, IQ3_S, 2048, 256, 128, 6, True, 4),
     # one token on the run-per-block launch A (the slot-by-slot one has no wave mapping for these): 17 slots, and
     # 9 slots of 4 pairs per block
     (IQ3_XXS, IQ3_S, 2048, 512, 128, 16, True, 1),

@@ -61,6 +61,7 @@ constexpr int kNormRowThreads = 1024;  // the norm launch: threads per token row
 constexpr int kSlabB = 64 * 1024;     // most LDS bytes of a chunk of groups' down rows (8 rows of each)
 constexpr int kBLoads = kSlabB / 16 / kThreadsB;  // 16-byte loads per thread in flight: a whole chunk
 constexpr int kHLoads = 3;            // 16-byte pieces of h per thread prefetched by launch B
+constexpr int kHLoadsT = 5;           // the same for fp32 h of several tokens (36 positions x 512: 4.5 per thread)
 constexpr int kItemsB = 2;            // launch B: (row, unit) items per thread decoded together
 static_assert(kMaxTok <= kThreadsA / 64, "one wave per token in the routing");
 
@@ -750,6 +751,256 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1s_kernel(LayerArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ launch A, a few tokens, group by group
+// Two to kTokT tokens: as layer_gu1s_kernel, every block takes the same pairs [q0, q1) of every expert the call
+// uses, so every CU has the same rows however the routing falls; but the rows are those of the groups (each distinct
+// expert once, with every entry that picked it, and the shared expert with every token), for at one token a row's
+// decode is the costly part and several tokens' picks coincide (correlated verify tokens: ~18 distinct experts of 32
+// picks).  Waves 0..T-1 route one token each; the last to finish groups the entries (layer_gu_kernel's order: expert
+// id, then entry) and publishes the group count in LDS, while waves kTokT..15 quantize every token's activations to
+// Q8_1 planes and store the codebook copies.  Then the block's rows - group g's row j, j < 2 ppb, the shared
+// expert's last - are dealt to the waves in turn, each wave requests all of its rows at once (at most kItemsT), and
+// dots each, decoded once, with every entry of its group.  h leaves in fp32 at the entries' positions in expert order,
+// the shared expert's at n_ent + t, as launch B reads them.
+constexpr int kTokT = 4;                 // tokens of this launch at most
+constexpr int kItemsT = 9;               // rows per wave at most (4 tokens x 8 picks + 1 shared, 4 rows each, over 16)
+constexpr int kRowsGB = 2;               // rows a wave decodes together (its slab)
+constexpr int kRowsGut = (kMaxEnt + kTokT) * 4;  // s_row: (position, row of the block) at most 2 ppb = 4 rows
+
+template <int GT, int CPR>
+__global__ void __launch_bounds__(kThreadsA) layer_gut_kernel(LayerArgs a) {
+#pragma clang fp contract(off)
+    constexpr int kHelp = kThreadsA - 64 * kTokT;  // the threads of waves kTokT..15
+    constexpr int RPH = (rep_stores<GT>() + kHelp - 1) / kHelp;
+    using Tab = std::conditional_t<(RPH > 0), RepTab<GT>, GridRef>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ int32_t s_ready;    // helper waves whose x planes and codebook copies are in LDS
+    __shared__ int32_t s_routed;   // routing waves done
+    __shared__ int32_t s_groups;   // the group count + 1 once the entries are grouped (0 before)
+    __shared__ int32_t s_ids[kMaxEnt], s_pos_ent[kMaxEnt], s_ent_pos[kMaxEnt];
+    __shared__ __attribute__((aligned(16))) int32_t s_key[kMaxEnt];  // the grouping's keys
+    __shared__ int32_t s_grp_expert[kMaxEnt], s_grp_start[kMaxEnt + 1];
+    __shared__ float s_pw[kMaxEnt];
+    __shared__ float s_row[kRowsGut];  // (position, row j of the block) -> its dot
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int k = a.k, T = a.n_tok, n_ent = T * k;
+    const tsx_expert_layout L = a.L;
+    const int N = (int) L.n_embd, NU = N / 32, FF = (int) L.n_ff;
+    const int sh = a.shared ? 1 : 0;
+    const int b = (int) blockIdx.x;
+    const int q0 = b * a.s1_ppb, np = a.s1_ppb, rs = 2 * np;  // no division in the prologue (layer_gu1s_kernel)
+    const int lrs = rs == 4 ? 2 : rs == 2 ? 1 : 0;              // rs is 2 or 4
+    const float rk = __builtin_amdgcn_rcpf((float) k);        // entry e -> token e / k (div_small)
+
+    if (tid == 0) s_ready = 0;
+    if (tid == 1) s_routed = 0;
+    if (tid == 2) s_groups = 0;
+    // 0. requested first: the routing waves their token's logits, the others the codebooks and the activations
+    float lg[kRouteV];
+    if (wave < T) route_fetch(a.logits + (int64_t) wave * a.n_expert, a.n_expert, lane, lg);
+    const int ht = tid - 64 * kTokT;
+    uint64_t rv[RPH > 0 ? RPH : 1];
+    if constexpr (RPH > 0)
+        if (wave >= kTokT) rep_fetch<GT, RPH>(rv, ht, kHelp);
+    const int nq_all = T * N / 4;
+    const float4* x4 = (const float4*) a.x;
+    float4 xv[kXLoads];
+#pragma unroll
+    for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(max(ht, 0) + kHelp * i, nq_all - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();  // the words above are set before any wave polls them
+    const uint64_t gu_row = L.gu_row;
+    const int ppr = (int) (gu_row / 16);
+    v4i* wslab = (v4i*) smem + wave * (kRowsGB * ppr);  // a batch of rows per wave
+    uint8_t* tabs = smem + (size_t) kWavesA * kRowsGB * gu_row;
+    int8_t* s_xq = (int8_t*) (tabs + rep_lds_bytes<GT>());
+    float* s_xd = (float*) (s_xq + (size_t) T * N);
+
+    // the entries' ranks in (expert, entry) order and the groups (layer_gu_kernel's grouping), by one wave
+    // (each entry's rank counted against the 64 keys read back from LDS four at a time - a loop of dependent
+    // readlanes took ~1 us - then the ids and entries moved to their ranks' lanes with ds_permute, a cross-lane push)
+    auto group = [&]() {
+        const int e = lane;
+        const int id = e < n_ent ? s_ids[e] : 0;
+        const int key = e < n_ent ? id * 64 + e : INT_MAX;
+        __hip_atomic_store(s_key + e, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");  // the wave's own stores, then its reads
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        int rank = 0;
+#pragma unroll
+        for (int q = 0; q < kMaxEnt / 4; ++q) {
+            const int4 v = ((const int4*) s_key)[q];
+            rank += (v.x < key) + (v.y < key) + (v.z < key) + (v.w < key);
+        }
+        const int dst = (e < n_ent ? rank : e) * 4;  // lanes past the entries keep their own place
+        const int xs = __builtin_amdgcn_ds_permute(dst, e < n_ent ? id : -1);
+        const int es = __builtin_amdgcn_ds_permute(dst, e);
+        if (e < n_ent) s_ent_pos[e] = rank;
+        if (lane < n_ent) s_pos_ent[lane] = es;
+        const int xp = lane < n_ent ? xs : -1;
+        const int xprev = __shfl_up(xs, 1, 64);
+        const bool start = lane < n_ent && (lane == 0 || xprev != xp);
+        const uint64_t mask = __ballot(start);
+        const int ng = __builtin_popcountll(mask);
+        if (start) {
+            const int g = __builtin_popcountll(mask & (~0ull >> (63 - lane))) - 1;
+            s_grp_expert[g] = xp;
+            s_grp_start[g] = lane;
+        }
+        if (lane == 0) s_grp_start[ng] = n_ent;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_store(&s_groups, ng + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
+
+    Tab grid;
+    if (wave < kTokT) {
+        if (wave < T) {
+            // 1. the routing of token `wave`, at raised issue priority; the last wave to finish groups the entries
+            __builtin_amdgcn_s_setprio(2);
+            route_select(lg, a.n_expert, k, lane, s_ids + wave * k, s_pw + wave * k);
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            int done = 0;
+            if (lane == 0) done = __hip_atomic_fetch_add(&s_routed, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            done = __builtin_amdgcn_readfirstlane(done);
+            if (done == T - 1) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                __builtin_amdgcn_s_setprio(2);
+                group();
+                __builtin_amdgcn_s_setprio(0);
+            }
+        }
+        if constexpr (RPH > 0) grid = rep_view<GT>(tabs);
+        else grid = grid_const();
+    } else {
+        // 1. every token's x into Q8_1 LDS planes and the codebook copies, while the routing waves route
+        for (int bq = 0; bq < nq_all; bq += kHelp * kXLoads) {
+            if (bq > 0) {
+#pragma unroll
+                for (int i = 0; i < kXLoads; ++i) xv[i] = x4[min(bq + ht + kHelp * i, nq_all - 1)];
+            }
+#pragma unroll
+            for (int i = 0; i < kXLoads; ++i) {
+                const int qd = bq + ht + kHelp * i;
+                if (bq + (ht & ~63) + kHelp * i < nq_all)  // whole waves
+                    q8_1_quad_to_lds(xv[i], qd < nq_all, s_xq + 4 * qd, s_xd + qd / 8, ht & 7);
+            }
+        }
+        if constexpr (RPH > 0) grid = rep_store<GT, RPH>(tabs, rv, ht, kHelp);
+        else grid = grid_const();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        if (lane == 0) __hip_atomic_fetch_add(&s_ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+
+    // 2. the groups, polled in LDS; the block's rows: item i = group i >> lrs (the shared expert as group ng), row
+    //    i & (rs - 1) of it, dealt to the waves in turn - the helpers first, the routing waves (done last) last
+    int g1;
+    while ((g1 = __hip_atomic_load(&s_groups, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) == 0)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    const int ng = g1 - 1, items = (ng + sh) << lrs;
+    const int wpos = wave >= kTokT ? wave - kTokT : wave + (kWavesA - kTokT);
+    // every wave requests kItemsT rows unconditionally (a row past its items repeats its last), so that the
+    // compiler's wait counts stay exact
+    v4i reg[kItemsT][CPR];
+    int it_g[kItemsT], it_j[kItemsT];
+#pragma unroll
+    for (int m = 0; m < kItemsT; ++m) {
+        const int i = min(wpos + kWavesA * m, items - 1);
+        const int g = i >> lrs, j = i & (rs - 1);
+        it_g[m] = g;
+        it_j[m] = j;
+        const uint8_t* blob = g < ng ? a.blobs + (uint64_t) s_grp_expert[g] * a.stride : a.shared;
+        const gbl_ptr<const v4i> src =
+            gbl_at<v4i>((uintptr_t) (blob + ((j & 1) ? L.up_off : 0) + (uint64_t) (q0 + j / 2) * gu_row));
+#pragma unroll
+        for (int c = 0; c < CPR; ++c) reg[m][c] = __builtin_nontemporal_load(src + min(lane + 64 * c, ppr - 1));
+    }
+    // x and the codebooks: every helper wave has counted itself in s_ready after its stores
+    while (__hip_atomic_load(&s_ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kWavesA - kTokT)
+        __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    // 3. the rows in batches of kRowsGB through the wave's slab, each unit of a row decoded once and dotted with
+    //    every entry of the row's group (the shared expert: every token); the batch's rows decode together
+#pragma unroll
+    for (int bb = 0; bb < (kItemsT + kRowsGB - 1) / kRowsGB; ++bb) {
+        const int m0 = bb * kRowsGB, left = items - (wpos + kWavesA * m0);
+        if (left <= 0) break;  // the same in every lane of the wave
+        const int nrow = min(kRowsGB, (left + kWavesA - 1) / kWavesA);
+        int lo[kRowsGB], n[kRowsGB];
+        bool shr[kRowsGB];
+#pragma unroll
+        for (int r = 0; r < kRowsGB; ++r) {
+            const int m = min(m0 + r, kItemsT - 1), g = it_g[m];
+            shr[r] = g >= ng;
+            lo[r] = g < ng ? s_grp_start[g] : 0;
+            n[r] = r < nrow ? (g < ng ? s_grp_start[g + 1] - lo[r] : T) : 0;
+#pragma unroll
+            for (int c = 0; c < CPR; ++c)
+                if (r < nrow && lane + 64 * c < ppr) wslab[r * ppr + lane + 64 * c] = reg[m][c];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the wave's LDS writes land before its reads
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        float acc[kRowsGB][kTokT] = {};
+        for (int u = lane; u < NU; u += 64) {
+            Unit w[kRowsGB];
+#pragma unroll
+            for (int r = 0; r < kRowsGB; ++r)
+                if (r < nrow) unit_load<GT>((const uint8_t*) (wslab + r * ppr), u, w[r], grid);
+#pragma unroll
+            for (int r = 0; r < kRowsGB; ++r) {
+#pragma unroll
+                for (int c = 0; c < kTokT; ++c) {
+                    if (c < n[r]) {
+                        // the entry's token (the shared expert: token c)
+                        const int tk = shr[r] ? c : div_small(s_pos_ent[lo[r] + c], k, rk);
+                        Act xa;
+                        act_planes(s_xq + (size_t) tk * N + 32 * u, s_xd + tk * NU + u, xa);
+                        int Sx, Mx;
+                        acc[r][c] += unit_dot<GT>(w[r], xa, Sx, Mx);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRowsGB; ++r) {
+            const int m = min(m0 + r, kItemsT - 1), j = it_j[m];
+#pragma unroll
+            for (int c = 0; c < kTokT; ++c) {
+                if (c < n[r]) {
+                    const float v = lanes_sum<64>(acc[r][c]);
+                    if (lane == 0) s_row[((shr[r] ? n_ent + c : lo[r] + c) << lrs) + j] = v;
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // the slab's reads are done before the next batch
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");  // overwrites it
+    }
+    __syncthreads();  // every dot is in s_row
+    // 4. h = silu(gate) * up per (position, pair), the product rounded on its own, in fp32 at the position
+    const int P = n_ent + (sh ? T : 0);
+    for (int i = tid; i < P * np; i += kThreadsA) {
+        const int pos = i / np, p = i - pos * np;
+        const float* row = s_row + (pos << lrs) + 2 * p;
+        const float gt = row[0];
+        a.hf[(int64_t) pos * FF + q0 + p] = (gt / (1.0f + expf(-gt))) * row[1];
+    }
+    if (b == 0) {
+        if (tid < n_ent) {
+            a.ids[tid] = s_ids[tid];
+            a.wts[tid] = s_pw[tid];
+            a.tab->wts[tid] = s_pw[tid];
+            a.tab->ent_pos[tid] = s_ent_pos[tid];
+        }
+        if (tid <= ng) {
+            if (tid < ng) a.tab->grp_expert[tid] = s_grp_expert[tid];
+            a.tab->grp_start[tid] = s_grp_start[tid];
+        }
+        if (tid == 0) a.tab->n_groups = ng;
+    }
+}
+
 // ------------------------------------------------------------------ launch B
 // Block b owns output rows [8 b, 8 b + 8).  It reads the tables and every entry's h in one round trip, then loads the
 // 8 rows of every used expert's down matrix (and the shared expert's: 8 contiguous rows each) into LDS with every
@@ -757,7 +1008,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1s_kernel(LayerArgs a) {
 // entries (tpr lanes per row, as many rows at once as the block has lanes for) and combines in pick order.
 // NR: rounds of 16-byte row loads per thread in flight (kBLoads, or 1 when a chunk's pieces fit one round: fewer
 // redundant clamped loads, and waits that stay exact)
-template <int DT, int NR>
+template <int DT, int NR, int HL = kHLoads>
 __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
 #pragma clang fp contract(off)
     constexpr int RP = (rep_stores<DT>() + kThreadsB - 1) / kThreadsB;
@@ -784,9 +1035,9 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     // h: the Q8_1 planes (16-byte pieces; n_ff is a multiple of 128), or fp32 h (float4 quads) quantized here
     const int nh = a.h_fp32 ? P * FF / 4 : (P * FF + P * NUd * 4) / 16;
     const v4i* hsrc = (const v4i*) (a.h_fp32 ? (const void*) a.hf : (const void*) a.hc);
-    v4i hv[kHLoads];
+    v4i hv[HL];
 #pragma unroll
-    for (int i = 0; i < kHLoads; ++i) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
+    for (int i = 0; i < HL; ++i) hv[i] = hsrc[min(tid + kThreadsB * i, nh - 1)];
     const float sg = a.shared ? a.sgate[(int64_t) min(tid, T - 1) * a.sg_stride] : 0.f;
     const int ty = min(tid / kRowsB, T - 1), ry = tid % kRowsB;  // the y value this thread combines into
     const float y0 = a.y[(int64_t) ty * N + r0 + ry];
@@ -829,12 +1080,12 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
         // and a wave with no quad left skips the round)
         const int w0 = tid & ~63;
 #pragma unroll
-        for (int i = 0; i < kHLoads; ++i) {
+        for (int i = 0; i < HL; ++i) {
             const int q = tid + kThreadsB * i;
             if (kThreadsB * i + w0 < nh)
                 q8_1_quad_to_lds(__builtin_bit_cast(float4, hv[i]), q < nh, s_hq + 4 * q, s_hd + q / 8, tid & 7);
         }
-        for (int base = kThreadsB * kHLoads; base + w0 < nh; base += kThreadsB) {
+        for (int base = kThreadsB * HL; base + w0 < nh; base += kThreadsB) {
             const int q = base + tid;
             q8_1_quad_to_lds(__builtin_bit_cast(float4, hsrc[min(q, nh - 1)]), q < nh, s_hq + 4 * q, s_hd + q / 8,
                              tid & 7);
@@ -842,9 +1093,9 @@ __global__ void __launch_bounds__(kThreadsB) layer_down_kernel(LayerArgs a) {
     } else {
         v4i* hdst = (v4i*) s_hq;
 #pragma unroll
-        for (int i = 0; i < kHLoads; ++i)
+        for (int i = 0; i < HL; ++i)
             if (tid + kThreadsB * i < nh) hdst[tid + kThreadsB * i] = hv[i];
-        for (int idx = tid + kThreadsB * kHLoads; idx < nh; idx += kThreadsB) hdst[idx] = hsrc[idx];
+        for (int idx = tid + kThreadsB * HL; idx < nh; idx += kThreadsB) hdst[idx] = hsrc[idx];
     }
     Tab grid;
     if constexpr (RP > 0) grid = rep_store<DT, RP>(smem + a.slab_b, rv, tid, kThreadsB);
@@ -1085,8 +1336,11 @@ extern "C" {
 
 TSX_API size_t tsx_moe_decode_layer_scratch_bytes(int n_tok, int k, int64_t n_ff) {
     if (n_tok < 1 || k < 1 || n_ff <= 0 || n_ff % 32 != 0) return 0;
-    // h as Q8_1 planes, or (one token) in fp32: k routed positions and the shared one
-    const size_t h = std::max(h_bytes(n_tok, k, n_ff), n_tok == 1 ? (size_t) (k + 1) * (size_t) n_ff * 4 : 0);
+    // h as Q8_1 planes, or in fp32 wherever a slot-by-slot launch A can take the call (one token; up to kTokT tokens
+    // at n_ff <= 2 kBlocksA, two rows of a slot per block): every routed position and every token's shared one
+    const bool fp32 = n_tok == 1 || (n_tok <= kTokT && n_ff <= 2 * kBlocksA);
+    const size_t h32 = fp32 ? (size_t) (n_tok * k + n_tok) * (size_t) n_ff * 4 : 0;
+    const size_t h = std::max(h_bytes(n_tok, k, n_ff), h32);
     return kTablesBytes + ((h + 255) & ~(size_t) 255);
 }
 
@@ -1117,7 +1371,9 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
     with_type(L.d_type, [&](auto T) {
         static const size_t limit = set_max_lds((const void*) layer_down_kernel<decltype(T)::value, kBLoads>);
         static const size_t limit1 = set_max_lds((const void*) layer_down_kernel<decltype(T)::value, 1>);
-        lim_b = std::min(limit, limit1);
+        static const size_t limit2 = set_max_lds((const void*) layer_down_kernel<decltype(T)::value, kBLoads, kHLoadsT>);
+        static const size_t limit3 = set_max_lds((const void*) layer_down_kernel<decltype(T)::value, 1, kHLoadsT>);
+        lim_b = std::min(std::min(limit, limit1), std::min(limit2, limit3));
         return 0;
     });
     const size_t fixed_a = rep_bytes(L.gu_type) + x_planes_bytes(L, n_tok);
@@ -1227,6 +1483,32 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
             });
         }
     }
+    if (n_tok >= 2 && n_tok <= kTokT && L.n_ff <= 2 * kBlocksA && L.gu_row % 16 == 0 &&
+        L.gu_row <= (uint64_t) 64 * 16 * 2) {
+        // a few tokens group by group: the block's rows of every group (at most one per routed entry, and the shared
+        // expert) dealt over the 16 waves, at most kItemsT each
+        const int nb = std::min(kBlocksA, (int) L.n_ff), ppb = (int) L.n_ff / nb, rs = 2 * ppb;
+        const int most = (n_tok * k + (shared ? 1 : 0)) * rs;
+        const int cpr = (int) ((L.gu_row / 16 + 63) / 64);
+        size_t limt = 0;
+        with_type(L.gu_type, [&](auto T) {
+            static const size_t l1 = set_max_lds((const void*) layer_gut_kernel<decltype(T)::value, 1>);
+            static const size_t l2 = set_max_lds((const void*) layer_gut_kernel<decltype(T)::value, 2>);
+            limt = std::min(l1, l2);
+            return 0;
+        });
+        const size_t ldst = (size_t) kWavesA * kRowsGB * L.gu_row + rep_bytes(L.gu_type) + x_planes_bytes(L, n_tok);
+        if (L.n_ff % nb == 0 && (rs == 2 || rs == 4) && most <= kWavesA * kItemsT && ldst <= limt) {
+            a.s1_ppb = ppb;
+            a.h_fp32 = 1;
+            a.rows_w = kRowsGB;
+            rc = with_type(L.gu_type, [&](auto T) {
+                if (cpr == 1) layer_gut_kernel<decltype(T)::value, 1><<<nb, kThreadsA, ldst, s>>>(a);
+                else layer_gut_kernel<decltype(T)::value, 2><<<nb, kThreadsA, ldst, s>>>(a);
+                return launch_status("tsx_moe_decode_layer/gate-up");
+            });
+        }
+    }
     if (!a.h_fp32)
         rc = with_type(L.gu_type, [&](auto T) {
             auto kern = layer_gu_kernel<decltype(T)::value>;
@@ -1241,7 +1523,11 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
     const int gb = (int) (kRowsB * L.d_row), gmax = std::min(n_tok * k, n_expert) + (shared ? 1 : 0);
     const bool one_round = (int64_t) std::min(std::max(1, slab_b / gb), gmax) * (gb / 16) <= kThreadsB;
     rc = with_type(L.d_type, [&](auto T) {
-        auto kern = one_round ? layer_down_kernel<decltype(T)::value, 1> : layer_down_kernel<decltype(T)::value, kBLoads>;
+        // fp32 h of several tokens: every piece requested in the first round (one more dependent round cost ~1 us)
+        const bool hl = a.h_fp32 && n_tok > 1;
+        auto kern = one_round ? (hl ? layer_down_kernel<decltype(T)::value, 1, kHLoadsT> : layer_down_kernel<decltype(T)::value, 1>)
+                              : (hl ? layer_down_kernel<decltype(T)::value, kBLoads, kHLoadsT>
+                                    : layer_down_kernel<decltype(T)::value, kBLoads>);
         const size_t lds = (size_t) slab_b + fixed_b;
         kern<<<(unsigned) (L.n_embd / kRowsB), kThreadsB, lds, s>>>(a);
         return launch_status("tsx_moe_decode_layer/down");

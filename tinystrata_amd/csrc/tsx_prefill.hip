@@ -457,6 +457,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     const int row0 = bounds[x] + s_tile0 * kBN;
     const int nrows = min(kBN, bounds[x + 1] - row0);
     const int ntt = (nrows + 15) >> 4;  // 16-token MFMA tiles with rows in them
+    // the tiles the chunk loop multiplies (the next size up in {1, 2, 3, 4, 6, 8}): only their activation pieces are
+    // loaded and staged, 256 16-byte pieces per tile (a multiple of 64, so the guards below are wave-uniform)
+    const int ntt_run = ntt <= 4 || kBN == 64 ? (kBN == 64 && ntt > 4 ? 4 : ntt) : ntt <= 6 ? 6 : 8;
+    const int plive = 256 * ntt_run;
     const int wrow = FUSE ? (BM / 2) * bx + 16 * wave : bx * CP * BM + 32 * wave;
     const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) wrow * row_bytes;
     // byte offset of the wave's row r (0-31) from wbase: FUSE rows 16-31 are the up rows of rows 0-15
@@ -502,7 +506,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
         for (int h = 0; h < BP; ++h) {
             const int pi = tid + NT * h, q = pi & 15;
-            av[h] = *(const v4i*) (P.q + (int64_t) arow_b[h] * P.cols + kChunk * c + 16 * q);
+            if (pi < plive) av[h] = *(const v4i*) (P.q + (int64_t) arow_b[h] * P.cols + kChunk * c + 16 * q);
         }
         if (tid < kBN) {
             const float4* dp = (const float4*) (P.d + (int64_t) arow_s * nu + 8 * c);
@@ -529,6 +533,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
         for (int h = 0; h < BP; ++h) {
             const int pi = tid + NT * h, rr = pi >> 4, q = pi & 15;
+            if (pi >= plive) continue;
             uint32_t o[8];
 #pragma unroll
             for (int k = 0; k < 4; ++k) i8_to_h((uint32_t) av[h][k], o[2 * k], o[2 * k + 1]);
