@@ -307,7 +307,7 @@ def run_config(args, name, cfg, steps, warmup, cpu, layers=None, cpu_seconds=Non
                                      ml.lscratch, shared=ml.W.shared, sgate=sg_d[l] if shared else None)
         dom_bytes = float(np.mean(layer_bytes))
         dom_ops = float(layer_ops)
-        kernel = ("tsx_moe_decode_layer (" + ("layer_gu1s_kernel" if T == 1 else "layer_gu_kernel") +
+        kernel = ("tsx_moe_decode_layer (" + ("layer_gu1s_kernel" if T == 1 else "layer_gut_kernel") +
                   " + layer_down_kernel) per layer")
     dom()
     torch.cuda.synchronize()
@@ -542,9 +542,9 @@ def summarize_trace(path: str, steps: int) -> str:
 
 # the dominant launch of each configuration by kernel (per layer for the decode configurations: both launches); where
 # one kernel runs at two grid sizes (the prompt products of the routed and the shared experts) the larger grid's
-DOMINANT = {"decode": ("layer_gu1s_kernel<18>", "layer_down_kernel<21, 1>"),
-            "plumb": ("layer_gu1s_kernel<8>", "layer_down_kernel<8, 4>"),
-            "verify": ("layer_gu_kernel<18>", "layer_down_kernel<21, 4>"),
+DOMINANT = {"decode": ("layer_gu1s_kernel<18>", "layer_down_kernel<21, 1, 3>"),
+            "plumb": ("layer_gu1s_kernel<8>", "layer_down_kernel<8, 4, 3>"),
+            "verify": ("layer_gut_kernel<18, 1>", "layer_down_kernel<21, 4, 5>"),
             "prefill": ("mmq_f16_kernel<12, 4, true, 1>",), "prefill_long": ("mmq_f16_kernel<18, 8, true, 1>",)}
 
 
