@@ -264,6 +264,13 @@ constexpr HalfTables make_half_tables() {
 static __constant__ const HalfTables kHalf = make_half_tables();
 template <int T> constexpr int half_grid_words() { return T == TSX_IQ3_XXS ? 512 : T == TSX_IQ3_S ? 1024 : 0; }
 template <int T> constexpr int half_table_words() { return 2 * half_grid_words<T>(); }
+// copies of the fp16 codebooks in LDS, interleaved entry by entry (entry i's copy c at slot i * copies + c; lane l
+// reads copy l % copies).  One: the lookups make about half of the product's LDS bank-conflict cycles (a timing copy
+// with lane-private lookup addresses ran the configs[4] gate/up 10 % faster), but eight copies, all the LDS beside the
+// tiles holds, cut the conflicts by 5 % only - lanes on the same copy still fall on the same few banks, and a lane of
+// its own per copy needs 32 of them
+template <int T> constexpr int tab_copies() { return 1; }
+template <int T> constexpr int rep_table_words() { return half_table_words<T>() * tab_copies<T>(); }
 
 constexpr int lds_round(int bytes) { return (bytes + 15) / 16 * 16; }
 template <int T> constexpr int chunk_bytes() { return T == TSX_Q8_0 ? 8 * 34 : Fmt<T>::bytes; }
@@ -273,7 +280,9 @@ template <int T> constexpr int chunk_bytes() { return T == TSX_Q8_0 ? 8 * 34 : F
 // experts are whole pieces apart - so it takes its own pieces only
 template <int T> constexpr bool chunk_aligned() { return chunk_bytes<T>() % 16 == 0; }
 template <int T> constexpr int raw_stride() {
-    return ((chunk_bytes<T>() + (chunk_aligned<T>() ? 0 : 15) + 15) / 16 | 1) * 16;
+    // a block of an even size starts at an even offset (the base, expert and row strides are multiples of 16 and the
+    // blocks even), so at most 14 bytes into its first piece
+    return ((chunk_bytes<T>() + (chunk_aligned<T>() ? 0 : chunk_bytes<T>() % 2 == 0 ? 14 : 15) + 15) / 16 | 1) * 16;
 }
 // silu(g) * u as the prompt path forms it (the fused gate/up epilogue and mmq_swiglu_kernel alike): g / (1 + e^-g)
 // with e^-g = 2^(-g log2 e) on the hardware exp2 and the quotient as g times the hardware reciprocal, the product
@@ -290,7 +299,7 @@ __device__ __forceinline__ float prompt_swiglu(float g, float u) {
 // compiler would order separate arrays by size, the large ones first)
 template <int T, int NW, int NB> struct F16Layout {
     static constexpr bool Q4K = T == TSX_Q4_K, Q80 = T == TSX_Q8_0, XXS = T == TSX_IQ3_XXS;
-    static constexpr int TW = half_table_words<T>();
+    static constexpr int TW = rep_table_words<T>();
     static constexpr int TAB = 0, AM = TAB + lds_round((TW > 0 ? TW : 4) * 4);
     static constexpr int SC = AM + lds_round((XXS ? NW : 1) * 8 * 32 * 8);
     static constexpr int UF = SC + lds_round((XXS ? 1 : NW) * 8 * 32 * 4);
@@ -381,7 +390,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     constexpr int NT = 64 * NW, BM = 32 * NW, NB = f16_buffers<T, NW>(), kBN = bn_of<T>();
     constexpr int CB = chunk_bytes<T>(), RS = raw_stride<T>(), PR = RS / 16, RW = (32 * PR + 63) / 64;
     constexpr int BP = kBN * 16 / NT, EPT = kMaxExpertsMmq / NT;
-    constexpr int TW = half_table_words<T>(), GW = half_grid_words<T>(), TPT = (TW + NT - 1) / NT;
+    constexpr int TC = tab_copies<T>(), TW = rep_table_words<T>(), GW = half_grid_words<T>(), TPT = (TW + NT - 1) / NT;
     constexpr bool Q4K = T == TSX_Q4_K, Q80 = T == TSX_Q8_0, IQ3S = T == TSX_IQ3_S;
     constexpr int XXS = T == TSX_IQ3_XXS;
     static_assert(kBN <= NT, "one thread per token stages the token's scales");
@@ -423,6 +432,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
         by = item / nbx;
     }
     const int lr = lane & 15, g = lane >> 4;
+    // this lane's copy of the codebooks (grid words, then sign entries)
+    const uint32_t* const gtab = &s_tab[0] + 2 * (lane % TC);
+    const uint32_t* const stab = &s_tab[0] + GW * TC + 4 * (lane % TC);
 
     // 1. which expert and which of its token tiles: EPT experts per thread, a block scan of tile counts.  The full
     // tiles of every expert are numbered first (expert order) and the partial last tiles after them, so that the
@@ -457,10 +469,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     const int row0 = bounds[x] + s_tile0 * kBN;
     const int nrows = min(kBN, bounds[x + 1] - row0);
     const int ntt = (nrows + 15) >> 4;  // 16-token MFMA tiles with rows in them
-    // the tiles the chunk loop multiplies (the next size up in {1, 2, 3, 4, 6, 8}): only their activation pieces are
-    // loaded and staged, 256 16-byte pieces per tile (a multiple of 64, so the guards below are wave-uniform)
-    const int ntt_run = ntt <= 4 || kBN == 64 ? (kBN == 64 && ntt > 4 ? 4 : ntt) : ntt <= 6 ? 6 : 8;
-    const int plive = 256 * ntt_run;
     const int wrow = FUSE ? (BM / 2) * bx + 16 * wave : bx * CP * BM + 32 * wave;
     const uint8_t* wbase = w + (uint64_t) x * expert_bytes + (uint64_t) wrow * row_bytes;
     // byte offset of the wave's row r (0-31) from wbase: FUSE rows 16-31 are the up rows of rows 0-15
@@ -506,7 +514,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
         for (int h = 0; h < BP; ++h) {
             const int pi = tid + NT * h, q = pi & 15;
-            if (pi < plive) av[h] = *(const v4i*) (P.q + (int64_t) arow_b[h] * P.cols + kChunk * c + 16 * q);
+            av[h] = *(const v4i*) (P.q + (int64_t) arow_b[h] * P.cols + kChunk * c + 16 * q);
         }
         if (tid < kBN) {
             const float4* dp = (const float4*) (P.d + (int64_t) arow_s * nu + 8 * c);
@@ -533,7 +541,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
 #pragma unroll
         for (int h = 0; h < BP; ++h) {
             const int pi = tid + NT * h, rr = pi >> 4, q = pi & 15;
-            if (pi >= plive) continue;
             uint32_t o[8];
 #pragma unroll
             for (int k = 0; k < 4; ++k) i8_to_h((uint32_t) av[h][k], o[2 * k], o[2 * k + 1]);
@@ -573,8 +580,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
         const uint32_t* sgn = T == TSX_IQ3_XXS ? kHalf.xxs_sign : kHalf.s_sign;
 #pragma unroll
         for (int k = 0; k < TPT; ++k) {
-            const int i = min(tid + NT * k, TW - 1);
-            tw[k] = i < GW ? src[i] : sgn[i - GW];
+            // word i of the copies: grid words first (entry, copy, word of two), then the sign entries (of four)
+            const int i = min(tid + NT * k, TW - 1), j = i - GW * TC;
+            tw[k] = j < 0 ? src[2 * (i / (2 * TC)) + (i & 1)] : sgn[4 * (j / (4 * TC)) + (j & 3)];
         }
     }
     if (tid < kBN) s_dl[tid] = 1.0f;   // read back only by the same thread (stage)
@@ -753,9 +761,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                     uint32_t f[4];
                     if constexpr (T == TSX_IQ3_XXS) {
                         const uint32_t qp = R.a[t][0], aux = R.a[t][1], m = R.a[t][2];
-                        const uint2 g0 = *(const uint2*) (s_tab + 2 * (qp & 255u));
-                        const uint2 g1 = *(const uint2*) (s_tab + 2 * (qp >> 8));
-                        const uint4 sm = *(const uint4*) (s_tab + GW + 4 * ((aux >> (7 * g)) & 127u));
+                        const uint2 g0 = *(const uint2*) (gtab + 2 * TC * (qp & 255u));
+                        const uint2 g1 = *(const uint2*) (gtab + 2 * TC * (qp >> 8));
+                        const uint4 sm = *(const uint4*) (stab + 4 * TC * ((aux >> (7 * g)) & 127u));
                         f[0] = hmul(g0.x ^ sm.x, m);
                         f[1] = hmul(g0.y ^ sm.y, m);
                         f[2] = hmul(g1.x ^ sm.z, m);
@@ -763,9 +771,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                     } else if constexpr (IQ3S) {
                         const uint32_t qp = R.a[t][0] & 0xFFFFu, qh = R.a[t][0] >> 16, m = R.a[t][2];
                         const uint32_t i0 = (qp & 255u) | (qh & 1u) << 8, i1 = (qp >> 8) | (qh & 2u) << 7;
-                        const uint2 g0 = *(const uint2*) (s_tab + 2 * i0);
-                        const uint2 g1 = *(const uint2*) (s_tab + 2 * i1);
-                        const uint4 sm = *(const uint4*) (s_tab + GW + 4 * R.a[t][1]);
+                        const uint2 g0 = *(const uint2*) (gtab + 2 * TC * i0);
+                        const uint2 g1 = *(const uint2*) (gtab + 2 * TC * i1);
+                        const uint4 sm = *(const uint4*) (stab + 4 * TC * R.a[t][1]);
                         f[0] = hmul(g0.x ^ sm.x, m);
                         f[1] = hmul(g0.y ^ sm.y, m);
                         f[2] = hmul(g1.x ^ sm.z, m);
