@@ -78,6 +78,18 @@ def test_decode_layer_scratch_covers_fp32_h():
         assert got >= planes and got < (T * k + T) * ff * 4, (T, k, ff, got)
 
 
+def test_decode_layer_refuses_a_short_scratch():
+    """The Python wrapper checks the scratch against the call's token count before any launch (a layer built for eight
+    tokens would hold Q8_1 planes only, too little for four tokens' fp32 h)."""
+    import torch
+    L = ops.native_expert_layout(_lib.IQ3_XXS, _lib.IQ3_S, 2048, 512)
+    x = torch.zeros(4, 2048)
+    short = torch.empty(ops.decode_layer_scratch_bytes(8, 8, 512) // 2, dtype=torch.uint8)
+    assert ops.decode_layer_scratch_bytes(4, 8, 512) > short.numel()
+    with pytest.raises(ValueError, match="scratch"):
+        ops.moe_decode_layer(L, None, 0, 256, 8, None, x, x, None, None, short)
+
+
 def test_supported_shapes():
     assert ops.native_expert_supported(_lib.IQ3_XXS, _lib.IQ3_S, 2048, 512)
     assert ops.native_expert_supported(_lib.Q4_K, _lib.Q4_K, 2048, 768)

@@ -126,6 +126,13 @@ def moe_decode_layer(L: ExpertLayout, blobs, stride: int, n_expert: int, k: int,
     """y += the whole decode MoE layer of x (1..8 tokens) in two launches (tsx_moe_decode_layer); with norm_w, also
     h = rms(y) * norm_w and (hq given) its Q8_1 image (tsx_moe_decode_layer_norm)."""
     n_tok = x.shape[0]
+    # the scratch size depends on the token count (h in fp32 for one to four tokens at n_ff <= 512, as Q8_1 planes
+    # otherwise): a buffer sized for another count may be too small
+    need = decode_layer_scratch_bytes(n_tok, k, int(L.n_ff))
+    have = scratch.numel() * scratch.element_size() if hasattr(scratch, "numel") else None
+    if have is not None and have < need:
+        raise ValueError(f"moe_decode_layer: scratch of {have} bytes, {n_tok} tokens x top-{k} at n_ff {int(L.n_ff)} "
+                         f"need {need} (decode_layer_scratch_bytes)")
     if norm_w is None:
         check(lib().tsx_moe_decode_layer(C.byref(L), _p(blobs), stride, n_expert, k, n_tok, _p(logits), _p(x),
                                          _p(shared), _p(sgate), sg_stride, _p(y), _p(ids), _p(wts), _p(scratch),
