@@ -311,7 +311,7 @@ template <int T, int NW, int NB> struct F16Layout {
     static constexpr int DL = RHO + lds_round(NB * 8 * 16 * RS * 4);
     static constexpr int DM = DL + lds_round(BN * 4);
     static constexpr int SCAN = DM + lds_round((Q4K ? NB * 8 * (BN + 16) : 1) * 4);
-    static constexpr int DR = SCAN + lds_round((NW + 2) * 4);
+    static constexpr int DR = SCAN + lds_round((NW + 1) * 8);
     static constexpr int RAW = DR + lds_round(BN * 4);
     static constexpr int TB = RAW + lds_round(NW * 32 * raw_stride<T>());
     static constexpr int BYTES = TB + NB * BN * kBStride * 2;
@@ -355,18 +355,18 @@ template <typename T> __device__ __forceinline__ lds_ptr<const T> lds_base(const
 __device__ __forceinline__ void wave_lds_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // exclusive prefix sum over the NT threads of the block (v per thread), and the total
-template <int NT>
-__device__ __forceinline__ int block_scan(int v, int* s_wave, int& total) {
+template <int NT, typename V>
+__device__ __forceinline__ V block_scan(V v, V* s_wave, V& total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int inc = v;
+    V inc = v;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int t = __shfl_up(inc, o, 64);
+        const V t = __shfl_up(inc, o, 64);
         if (lane >= o) inc += t;
     }
     if (lane == 63) s_wave[wave] = inc;
     __syncthreads();
-    int off = 0;
+    V off = 0;
     total = 0;
 #pragma unroll
     for (int w = 0; w < NT / 64; ++w) {
@@ -410,57 +410,64 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     // Q4_K min-term factors: rows of kBN + 16 floats, so that lane groups 0 and 1 (units 4 h, 4 h + 1) of one
     // 32-lane half read different banks
     auto& s_dm = *reinterpret_cast<float(*)[Q4K ? NB : 1][8][Q4K ? kBN + 16 : 1]>(s_lds + L::DM);
-    int* const s_scan = reinterpret_cast<int*>(s_lds + L::SCAN);
-    int& s_x = s_scan[NW];
-    int& s_tile0 = s_scan[NW + 1];
+    uint64_t* const s_scan = reinterpret_cast<uint64_t*>(s_lds + L::SCAN);
+    int& s_x = reinterpret_cast<int*>(s_scan + NW)[0];
+    int& s_tile0 = reinterpret_cast<int*>(s_scan + NW)[1];
     int* const s_drow = reinterpret_cast<int*>(s_lds + L::DR);  // the output row of each token of the tile
     auto& s_raw = *reinterpret_cast<uint8_t(*)[NW][32 * RS]>(s_lds + L::RAW);
     auto& tB = *reinterpret_cast<_Float16(*)[NB][kBN * kBStride]>(s_lds + L::TB);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Which (column block bx, token tile by): workgroups go to the 8 XCDs in turn by their linear index, so with
-    // tpg > 0 the s-th block to reach XCD x takes item ((s / G) * 8 + x) * G + s % G of the (tile-major) items,
-    // G = gridDim.x * tpg: runs of tpg consecutive tiles, all their column blocks, share an XCD and its L2 (a tile's
-    // activation rows serve every column block, and an expert's weights its next tiles), while the runs still come in
-    // tile order over the whole chip.  The host pads gridDim.y to a multiple of 8 tpg (a bijection on the grid).
+    // Which (column block bx, token tile by), set once the tiles are counted (step 1): workgroups go to the 8 XCDs in
+    // turn by their linear index, so with tpg > 0 the s-th block to reach XCD x takes item ((s / G) * 8 + x) * G +
+    // s % G of the (tile-major) items, G = gridDim.x * tpg: runs of tpg consecutive tiles, all their column blocks,
+    // share an XCD and its L2 (a tile's activation rows serve every column block, and an expert's weights its next
+    // tiles), while the runs still come in tile order over the whole chip.  The map is a bijection on each 8 G
+    // items, and applies to the whole rounds of 8 G items that full tiles fill.
     int bx = blockIdx.x, by = blockIdx.y;
-    if (tpg > 0) {
-        const int nbx = (int) gridDim.x, lin = bx + nbx * by, G = nbx * tpg;
-        const int xcd = lin & 7, sx = lin >> 3;
-        const int item = ((sx / G) * 8 + xcd) * G + sx % G;
-        bx = item % nbx;
-        by = item / nbx;
-    }
     const int lr = lane & 15, g = lane >> 4;
     // this lane's copy of the codebooks (grid words, then sign entries)
     const uint32_t* const gtab = &s_tab[0] + 2 * (lane % TC);
     const uint32_t* const stab = &s_tab[0] + GW * TC + 4 * (lane % TC);
 
-    // 1. which expert and which of its token tiles: EPT experts per thread, a block scan of tile counts.  The full
-    // tiles of every expert are numbered first (expert order) and the partial last tiles after them, so that the
-    // hardware dispatches the long blocks first and the short ones fill the end of the launch.  Counts travel
-    // packed: full tiles in the low 16 bits, partial tiles in the high 16 (each total is at most 32768 / 64)
-    int tc[EPT], mine = 0;
+    // 1. which expert and which of its token tiles: EPT experts per thread, a block scan of tile counts.  Tiles are
+    // numbered by their length, longest first, so that the hardware dispatches the long blocks first and the short
+    // ones fill the end of the launch: the full tiles of every expert (expert order), then the partial last tiles of
+    // more than kBN / 4 rows, then the shorter ones.  Counts travel packed in 16-bit fields (full, long partial,
+    // short partial; a total is at most gridDim.y < 2^16)
+    constexpr int kShort = kBN / 4;
+    uint64_t tc[EPT], mine = 0;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const int x = EPT * tid + e;
         const int b0 = bounds[min(x, n_exp)], b1 = bounds[min(x + 1, n_exp)];
-        const int rows = x < n_exp ? b1 - b0 : 0;
-        tc[e] = rows / kBN | (rows % kBN != 0 ? 1 << 16 : 0);
+        const int rows = x < n_exp ? b1 - b0 : 0, rest = rows % kBN;
+        tc[e] = (uint64_t) (rows / kBN) | (uint64_t) (rest > kShort) << 16 | (uint64_t) (rest > 0 && rest <= kShort) << 32;
         mine += tc[e];
     }
-    int total;
-    int start = block_scan<NT>(mine, s_scan, total);
-    const int nfull = total & 0xFFFF;
-    if (by >= nfull + (total >> 16)) return;  // the whole block: fewer tiles than the grid's upper bound
-    const bool part = by >= nfull;
-    const int want = part ? by - nfull : by;
+    uint64_t total;
+    uint64_t start = block_scan<NT>(mine, s_scan, total);
+    const int nfull = (int) (total & 0xFFFF), nlong = (int) (total >> 16 & 0xFFFF);
+    // the XCD order over the whole rounds of full tiles; the rest (the last full tiles and the partial
+    // tiles, one per expert, whose weights no other tile shares) in linear order, longest first over the whole chip
+    if (tpg > 0) {
+        const int nbx = (int) gridDim.x, lin = bx + nbx * by, G = nbx * tpg;
+        if (lin < nfull / (8 * tpg) * 8 * G) {
+            const int xcd = lin & 7, sx = lin >> 3;
+            const int item = ((sx / G) * 8 + xcd) * G + sx % G;
+            bx = item % nbx;
+            by = item / nbx;
+        }
+    }
+    if (by >= nfull + nlong + (int) (total >> 32)) return;  // the whole block: fewer tiles than the grid's upper bound
+    const int cls = by < nfull ? 0 : by < nfull + nlong ? 1 : 2;  // full, long partial, short partial
+    const int want = by - (cls > 0 ? nfull : 0) - (cls > 1 ? nlong : 0);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-        const int s0 = part ? start >> 16 : start & 0xFFFF, n = part ? tc[e] >> 16 : tc[e] & 0xFFFF;
+        const int s0 = (int) (start >> (16 * cls) & 0xFFFF), n = (int) (tc[e] >> (16 * cls) & 0xFFFF);
         if (s0 <= want && want < s0 + n) {
             s_x = EPT * tid + e;
-            s_tile0 = part ? tc[e] & 0xFFFF : want - s0;  // the tile's index within its expert
+            s_tile0 = cls > 0 ? (int) (tc[e] & 0xFFFF) : want - s0;  // the tile's index within its expert
         }
         start += tc[e];
     }
