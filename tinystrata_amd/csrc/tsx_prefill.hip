@@ -433,21 +433,21 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     // 1. which expert and which of its token tiles: EPT experts per thread, a block scan of tile counts.  Tiles are
     // numbered by their length, longest first, so that the hardware dispatches the long blocks first and the short
     // ones fill the end of the launch: the full tiles of every expert (expert order), then the partial last tiles of
-    // more than kBN / 4 rows, then the shorter ones.  Counts travel packed in 16-bit fields (full, long partial,
-    // short partial; a total is at most gridDim.y < 2^16)
-    constexpr int kShort = kBN / 4;
+    // more than kBN / 2 rows, of more than kBN / 4, and the shorter ones.  Counts travel packed in four 16-bit fields
+    // (a total is at most gridDim.y < 2^16)
     uint64_t tc[EPT], mine = 0;
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const int x = EPT * tid + e;
         const int b0 = bounds[min(x, n_exp)], b1 = bounds[min(x + 1, n_exp)];
         const int rows = x < n_exp ? b1 - b0 : 0, rest = rows % kBN;
-        tc[e] = (uint64_t) (rows / kBN) | (uint64_t) (rest > kShort) << 16 | (uint64_t) (rest > 0 && rest <= kShort) << 32;
+        const int cl = rest > kBN / 2 ? 1 : rest > kBN / 4 ? 2 : 3;  // the partial tile's field
+        tc[e] = (uint64_t) (rows / kBN) | (uint64_t) (rest > 0) << (16 * cl);
         mine += tc[e];
     }
     uint64_t total;
     uint64_t start = block_scan<NT>(mine, s_scan, total);
-    const int nfull = (int) (total & 0xFFFF), nlong = (int) (total >> 16 & 0xFFFF);
+    const int nfull = (int) (total & 0xFFFF);
     // the XCD order over the whole rounds of full tiles; the rest (the last full tiles and the partial
     // tiles, one per expert, whose weights no other tile shares) in linear order, longest first over the whole chip
     if (tpg > 0) {
@@ -459,9 +459,17 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
             by = item / nbx;
         }
     }
-    if (by >= nfull + nlong + (int) (total >> 32)) return;  // the whole block: fewer tiles than the grid's upper bound
-    const int cls = by < nfull ? 0 : by < nfull + nlong ? 1 : 2;  // full, long partial, short partial
-    const int want = by - (cls > 0 ? nfull : 0) - (cls > 1 ? nlong : 0);
+    // the tile's class (0 full, 1-3 partial) and its index among the class's tiles
+    int cls = 0, want = by;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int n = (int) (total >> (16 * k) & 0xFFFF);
+        if (cls == k && want >= n) {
+            want -= n;
+            ++cls;
+        }
+    }
+    if (cls == 4) return;  // the whole block: fewer tiles than the grid's upper bound
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
         const int s0 = (int) (start >> (16 * cls) & 0xFFFF), n = (int) (tc[e] >> (16 * cls) & 0xFFFF);
