@@ -1102,10 +1102,12 @@ TSX_API int tsx_moe_mmq_quantize_route(const float* x, void* xq, int type, int64
     return launch_status("tsx_moe_mmq_quantize_route");
 }
 
-// runs of kXcdTiles consecutive token tiles per XCD (mmq_f16_kernel's tpg); the tile grid padded to whole rounds of
-// runs over the 8 XCDs, its extra blocks returning at once like the tiles past the routing's count
-// (2 measured best of 0, 1, 2, 4, 8: configs[3] gate/up 168 -> 162 us, configs[4] 345.5 -> 343 us; 8 lost 10 %)
-constexpr int kXcdTiles = 2;
+// runs of kXcdTiles consecutive token tiles per XCD (mmq_f16_kernel's tpg) over the whole rounds of full tiles; the
+// tile grid padded to whole rounds of runs over the 8 XCDs, its extra blocks returning at once like the tiles past the
+// routing's count.  With every tile in the runs, 2 measured best of 0, 1, 2, 4, 8 (configs[3] gate/up 168 -> 162 us,
+// configs[4] 345.5 -> 343 us; 8 lost 10 %); with the partial tiles outside them, 4 against 2: configs[4] gate/up
+// 344.5 -> 337.3 us, configs[3] 136.1 -> 135.1 us, and 8 within 1 % of 4
+constexpr int kXcdTiles = 4;
 inline int64_t xcd_tiles(int64_t tiles) { return (tiles + 8 * kXcdTiles - 1) / (8 * kXcdTiles) * (8 * kXcdTiles); }
 
 TSX_API int tsx_moe_mmq_run(const tsx_mmq_product* p, void* stream) {
