@@ -381,6 +381,39 @@ def test_mmq_run_skewed_groups(t, w_cols, w_rows):
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * np.abs(exp).max())
 
 
+@pytest.mark.parametrize("t", [IQ3_XXS, Q4_K])
+def test_mmq_run_tile_classes(t):
+    """The block order's tile classes at their edges: partial last tiles of exactly kBN/4 and kBN/2 rows and one more
+    (IQ3: 128-token tiles, Q4_K: 64), whole tiles, empty experts, and enough full tiles (two experts of 1500 and 2600
+    rows) that whole rounds of them take the XCD order while the rest keep linear order; every sorted row once, against
+    the oracle's per-row dot on the same Q8_1 codes."""
+    w_cols, w_rows = 512, 256
+    rng = np.random.default_rng(40 + t)
+    counts = [16, 17, 32, 33, 0, 48, 64, 65, 2600, 96, 127, 128, 160, 161, 80, 1500, 1, 0, 31]
+    n, total = len(counts), sum(counts)
+    bounds = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    W = [ops.quantize_weights(t, rng.normal(0, 0.02, (w_rows, w_cols)).astype(np.float32)) for _ in range(n)]
+    rb = W[0].shape[1]
+    eb = (w_rows * rb + 255) // 256 * 256
+    blob = np.zeros(n * eb, np.uint8)
+    for i, m in enumerate(W):
+        blob[i * eb: i * eb + m.size] = m.ravel()
+    x = rng.normal(0, 1, (total, w_cols)).astype(np.float32)
+    ids = rng.permutation(total).astype(np.int32)
+    xq = ops.mmq_quantize(dev(x), None, t, w_cols, w_cols, total)
+    dst = torch.full((total, w_rows), float("nan"), device="cuda")
+    ops.mmq_run(dev(blob), t, w_rows, w_cols, eb, n, xq, dev(bounds), dev(ids), total, dst, w_rows)
+    got = host(dst)
+    xb = O.quantize_q8_1(x)
+    exp = np.zeros((total, w_rows), np.float64)
+    for i in range(n):
+        r0, r1 = bounds[i], bounds[i + 1]
+        if r1 > r0:
+            exp[ids[r0:r1]] = O.mmvq_q8_1(t, W[i], w_cols, w_rows, xb[r0:r1], r1 - r0)
+    assert np.isfinite(got).all()  # every row written (the NaN fill would survive a missed tile)
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5 * np.abs(exp).max())
+
+
 def _planes(buf, rows: int, cols: int):
     """The Q8_1 planes of tsx_moe_mmq_q8_bytes: codes, block scales and code sums of the first `rows` rows."""
     b = host(buf)
