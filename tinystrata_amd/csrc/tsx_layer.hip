@@ -764,6 +764,9 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1s_kernel(LayerArgs a) {
 // the shared expert's at n_ent + t, as launch B reads them.
 constexpr int kTokT = 4;                 // tokens of this launch at most
 constexpr int kItemsT = 9;               // rows per wave at most (4 tokens x 8 picks + 1 shared, 4 rows each, over 16)
+// rows per wave at most for rows of CPR 16-byte pieces per lane: rows of over 1 KB hold twice the registers in flight
+// per row, and nine (seven, IQ3_S) of them spilled
+template <int CPR> constexpr int items_t() { return CPR == 1 ? kItemsT : 6; }
 constexpr int kRowsGB = 2;               // rows a wave decodes together (its slab)
 constexpr int kRowsGut = (kMaxEnt + kTokT) * 4;  // s_row: (position, row of the block) at most 2 ppb = 4 rows
 
@@ -901,12 +904,13 @@ __global__ void __launch_bounds__(kThreadsA) layer_gut_kernel(LayerArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     const int ng = g1 - 1, items = (ng + sh) << lrs;
     const int wpos = wave >= kTokT ? wave - kTokT : wave + (kWavesA - kTokT);
-    // every wave requests kItemsT rows unconditionally (a row past its items repeats its last), so that the
+    constexpr int IT = items_t<CPR>();
+    // every wave requests IT rows unconditionally (a row past its items repeats its last), so that the
     // compiler's wait counts stay exact
-    v4i reg[kItemsT][CPR];
-    int it_g[kItemsT], it_j[kItemsT];
+    v4i reg[IT][CPR];
+    int it_g[IT], it_j[IT];
 #pragma unroll
-    for (int m = 0; m < kItemsT; ++m) {
+    for (int m = 0; m < IT; ++m) {
         const int i = min(wpos + kWavesA * m, items - 1);
         const int g = i >> lrs, j = i & (rs - 1);
         it_g[m] = g;
@@ -924,7 +928,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gut_kernel(LayerArgs a) {
     // 3. the rows in batches of kRowsGB through the wave's slab, each unit of a row decoded once and dotted with
     //    every entry of the row's group (the shared expert: every token); the batch's rows decode together
 #pragma unroll
-    for (int bb = 0; bb < (kItemsT + kRowsGB - 1) / kRowsGB; ++bb) {
+    for (int bb = 0; bb < (IT + kRowsGB - 1) / kRowsGB; ++bb) {
         const int m0 = bb * kRowsGB, left = items - (wpos + kWavesA * m0);
         if (left <= 0) break;  // the same in every lane of the wave
         const int nrow = min(kRowsGB, (left + kWavesA - 1) / kWavesA);
@@ -932,7 +936,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gut_kernel(LayerArgs a) {
         bool shr[kRowsGB];
 #pragma unroll
         for (int r = 0; r < kRowsGB; ++r) {
-            const int m = min(m0 + r, kItemsT - 1), g = it_g[m];
+            const int m = min(m0 + r, IT - 1), g = it_g[m];
             shr[r] = g >= ng;
             lo[r] = g < ng ? s_grp_start[g] : 0;
             n[r] = r < nrow ? (g < ng ? s_grp_start[g + 1] - lo[r] : T) : 0;
@@ -965,7 +969,7 @@ __global__ void __launch_bounds__(kThreadsA) layer_gut_kernel(LayerArgs a) {
         }
 #pragma unroll
         for (int r = 0; r < kRowsGB; ++r) {
-            const int m = min(m0 + r, kItemsT - 1), j = it_j[m];
+            const int m = min(m0 + r, IT - 1), j = it_j[m];
 #pragma unroll
             for (int c = 0; c < kTokT; ++c) {
                 if (c < n[r]) {
@@ -1486,7 +1490,7 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
     if (n_tok >= 2 && n_tok <= kTokT && L.n_ff <= 2 * kBlocksA && L.gu_row % 16 == 0 &&
         L.gu_row <= (uint64_t) 64 * 16 * 2) {
         // a few tokens group by group: the block's rows of every group (at most one per routed entry, and the shared
-        // expert) dealt over the 16 waves, at most kItemsT each
+        // expert) dealt over the 16 waves, at most items_t<cpr>() each
         const int nb = std::min(kBlocksA, (int) L.n_ff), ppb = (int) L.n_ff / nb, rs = 2 * ppb;
         const int most = (n_tok * k + (shared ? 1 : 0)) * rs;
         const int cpr = (int) ((L.gu_row / 16 + 63) / 64);
@@ -1498,7 +1502,8 @@ static int decode_layer(const tsx_expert_layout* Lp, const void* blobs, uint64_t
             return 0;
         });
         const size_t ldst = (size_t) kWavesA * kRowsGB * L.gu_row + rep_bytes(L.gu_type) + x_planes_bytes(L, n_tok);
-        if (L.n_ff % nb == 0 && (rs == 2 || rs == 4) && most <= kWavesA * kItemsT && ldst <= limt) {
+        if (L.n_ff % nb == 0 && (rs == 2 || rs == 4) && most <= kWavesA * (cpr == 1 ? items_t<1>() : items_t<2>()) &&
+            ldst <= limt) {
             a.s1_ppb = ppb;
             a.h_fp32 = 1;
             a.rows_w = kRowsGB;
