@@ -650,10 +650,8 @@ __device__ __forceinline__ void route_select_v(const float (&lv)[kRouteV], int k
         // in several lanes) the smallest of their ids
         const uint32_t wm = wave_max_u32(key[0]);
         const uint64_t hit = __ballot(key[0] == wm);
-        int x;
-        if (__builtin_popcountll(hit) == 1)
-            x = __builtin_amdgcn_readlane((int) id[0], (int) __builtin_ctzll(hit));
-        else
+        int x = __builtin_amdgcn_readlane((int) id[0], (int) __builtin_ctzll(hit));
+        if (__builtin_expect(__builtin_popcountll(hit) != 1, 0))
             x = (int) wave_min_u32(key[0] == wm ? id[0] : 0xFFFFFFFFu);
         const bool win = lane == (x & 63);
 #pragma unroll
@@ -675,7 +673,7 @@ __device__ __forceinline__ void route_select_v(const float (&lv)[kRouteV], int k
         wts[lane] = my_p * inv;
     }
 }
-// route_select_v's rounds with each pick published as it is found: lane 0 stores pick r + 1 into pub[r] (LDS words
+// route_select_v's rounds with each pick published as it is found: the wave stores pick r + 1 into pub[r] (LDS words
 // that start at 0, so a reader polls for a nonzero word) with a relaxed workgroup-scope atomic store, which is a plain
 // ds_write (a volatile store through a generic pointer became a system-coherent flat store and a wait for it, a memory
 // round trip in every round), and after round 0 the whole wave calls after0().  ids / wts as route_select_v, written
@@ -690,12 +688,13 @@ __device__ __forceinline__ void route_publish_v(const float (&lv)[kRouteV], int 
     for (int r = 0; r < k; ++r) {
         const uint32_t wm = wave_max_u32(key[0]);
         const uint64_t hit = __ballot(key[0] == wm);
-        int x;
-        if (__builtin_popcountll(hit) == 1)
-            x = __builtin_amdgcn_readlane((int) id[0], (int) __builtin_ctzll(hit));
-        else
+        // the one lane holding it (the common case, no branch taken), or, equal heads in several lanes, the smallest
+        // of their ids
+        int x = __builtin_amdgcn_readlane((int) id[0], (int) __builtin_ctzll(hit));
+        if (__builtin_expect(__builtin_popcountll(hit) != 1, 0))
             x = (int) wave_min_u32(key[0] == wm ? id[0] : 0xFFFFFFFFu);
-        if (lane == 0) __hip_atomic_store(pub + r, x + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        // every lane stores the same word: no exec-mask branch in the round (stamps: the eight rounds 0.3 us sooner)
+        __hip_atomic_store(pub + r, x + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         const bool win = lane == (x & 63);
 #pragma unroll
         for (int i = 0; i + 1 < V; ++i) {
