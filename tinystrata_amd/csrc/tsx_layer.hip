@@ -653,10 +653,13 @@ __global__ void __launch_bounds__(kThreadsA) layer_gu1s_kernel(LayerArgs a) {
                 acc[j] += unit_dot<GT>(w[j], xa, Sx, Mx);
             }
         }
+        // every row's 64-lane sum first, so that the reduction chains interleave, then lane 0's stores
+        float v[R];
 #pragma unroll
-        for (int j = 0; j < R; ++j) {
-            const float v = lanes_sum<64>(acc[j]);
-            if (lane == 0) s_row[slot * rs + j0 + j] = v;
+        for (int j = 0; j < R; ++j) v[j] = lanes_sum<64>(acc[j]);
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < R; ++j) s_row[slot * rs + j0 + j] = v[j];
         }
     };
     // the slot's pick, polled in LDS until wave 0 has published it (relaxed atomic loads: a fresh ds_read every time
