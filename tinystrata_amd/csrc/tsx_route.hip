@@ -135,8 +135,12 @@ __global__ void __launch_bounds__(kSortThreads) route_sort_kernel(const int32_t*
     __shared__ int s_wsum[kSortWaves], s_wmax[kSortWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile0 = blockIdx.x * kSortThreads;
-    for (int i = tid; i < kSortWaves * n_expert; i += kSortThreads) wcnt[i / n_expert][i % n_expert] = 0;
-    __syncthreads();
+    // this thread's own entry of the tile, requested first (its scatter comes last)
+    const int e = tile0 + tid;
+    int x = e < n_ent ? ids[e] : -1;
+    // each wave clears its own counts (only it adds to them, below): no division and no block barrier
+    for (int xx = lane; xx < n_expert; xx += 64) wcnt[wave][xx] = 0;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     // every entry's expert counted (a wave's 64 entries lie in one tile) in entries [lo, hi), kSortBatch tiles' ids
     // requested at once so that one load latency covers them
     auto count = [&](int lo, int hi) {
@@ -203,8 +207,6 @@ __global__ void __launch_bounds__(kSortThreads) route_sort_kernel(const int32_t*
         }
     }
     // this tile's entries, stably
-    const int e = tile0 + tid;
-    int x = e < n_ent ? ids[e] : -1;
     if (x < 0 || x >= n_expert) x = -1;
     const uint64_t same = same_expert(x);
     const int rank = __builtin_popcountll(same & ((1ull << lane) - 1ull));
